@@ -1,0 +1,105 @@
+// Device-side geometry and bit-exact scalar codec helpers shared by the
+// pack, reconstruct and decode kernels (gfx950 / CDNA4, wave64).
+//
+// Record geometry (docs/agents/numerical-and-validation.md:10-12 in the
+// reference): 512 coordinates = 448 NoPE + 64 RoPE tail; Packed keeps 256 as
+// E4M3 codes + a 512-bit bitmap + 8 UE8M0 scales = 328 bytes. A page holds 64
+// records: the 64 data rows (codes, then bitmap; 320 bytes) followed by the 64
+// scale rows (8 bytes), so every data row starts on a 16-byte boundary.
+// Native records are 584 bytes: 448 E4M3 codes + 64 rotated BF16 + 8 scales,
+// paged the same way (576-byte data rows, then 8-byte scale rows).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rm {
+
+constexpr int kHeadDim = 512;
+constexpr int kNopeDim = 448;
+constexpr int kRopePairs = 32;
+constexpr int kKeep = 256;
+constexpr int kGroup = 64;
+constexpr int kCodeBytes = 256;
+constexpr int kBitmapBytes = 64;
+constexpr int kDataBytes = kCodeBytes + kBitmapBytes;   // 320
+constexpr int kScaleBytes = 8;
+constexpr int kPageRecords = 64;
+constexpr int kPageBytes = kPageRecords * (kDataBytes + kScaleBytes);        // 20992
+constexpr int kNativeDataBytes = kNopeDim + 2 * (kHeadDim - kNopeDim);       // 576
+constexpr int kNativePageBytes = kPageRecords * (kNativeDataBytes + kScaleBytes);  // 37376
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// float -> bf16 bits, round to nearest even (inputs are finite here).
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+  uint32_t u = f2u(f);
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return u2f(h << 16); }
+
+// OCP E4M3 (e4m3fn) encode, round to nearest even, |q| <= 448 by construction.
+__device__ __forceinline__ uint32_t e4m3_rne(float q) {
+  uint32_t b = f2u(q);
+  uint32_t sign = (b >> 24) & 0x80u;
+  uint32_t ab = b & 0x7fffffffu;
+  uint32_t code;
+  if (u2f(ab) < 0x1p-6f) {
+    code = (uint32_t)(int)__builtin_rintf(u2f(ab) * 512.0f);  // subnormal: m * 2^-9
+  } else {
+    uint32_t r = ab + 0x7ffffu + ((ab >> 20) & 1u);
+    code = (r >> 20) - ((127u - 7u) << 3);
+  }
+  return sign | code;
+}
+
+// E4M3 code -> float (exact).
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  uint32_t e = (c >> 3) & 15u, m = c & 7u;
+  float v = e ? u2f(((e + 120u) << 23) | (m << 20)) : (float)m * 0x1p-9f;
+  return (c & 0x80u) ? -v : v;
+}
+
+// UE8M0 exponent: smallest e with max(amax, 1e-4) <= 448 * 2^e, i.e.
+// ceil(log2(max(amax, 1e-4) / 448)).
+__device__ __forceinline__ int ue8m0_exponent(float amax) {
+  if (!(amax >= 1e-4f)) return -22;
+  uint32_t b = f2u(amax);
+  return (int)((b >> 23) & 0xffu) - 127 - 8 + ((b & 0x7fffffu) > 0x600000u ? 1 : 0);
+}
+
+// 2^e as a float for e in [-126, 127].
+__device__ __forceinline__ float exp2i(int e) { return u2f((uint32_t)(e + 127) << 23); }
+
+__device__ __forceinline__ int wave_lane() { return (int)(threadIdx.x & 63u); }
+
+// Make a per-wave value provably uniform (scalar register).
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Order LDS writes of a wave before later reads by other lanes of the same wave.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Tail rotation of 4 interleaved (re, im) pairs held as floats, with
+// (cos, sin) pairs from the frequency table: re' = xr*c - xi*s, im' = xr*s + xi*c,
+// every product rounded (compiled without FMA contraction).
+__device__ __forceinline__ void rope4(float* v, const float* cs) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float xr = v[2 * j], xi = v[2 * j + 1], c = cs[2 * j], s = cs[2 * j + 1];
+    float a = xr * c, b = xi * s;
+    float d = xr * s, e = xi * c;
+    v[2 * j] = a - b;
+    v[2 * j + 1] = d + e;
+  }
+}
+
+}  // namespace rm

@@ -1,0 +1,326 @@
+// Store kernels: Packed C4 record packer and the Native 584-byte control store.
+//
+// One wave64 per record; lane l owns coordinates 8l..8l+7 (16-byte BF16 or
+// 32-byte FP32 loads, so a wave reads the 512-coordinate row in one coalesced
+// sweep). No MFMA: the work is per-record selection, reductions and bit packing.
+//
+// Packed arithmetic (reference: training/losses.py:84-95, evaluate.py:65-91,
+// test_integration.py:1588-1619; producer order in
+// docs/agents/numerical-and-validation.md:22-26):
+//   1. keep the 256 largest |x| (raw magnitudes); ties keep lower coordinates;
+//   2. m = masked x; r = RN(1/RN(sqrt(sum(m^2)/512 + eps))), sum in the fixed
+//      lane-then-pairwise-tree order; n = bf16(RN(RN(m*r)*w));
+//   3. per 64-coordinate group: e = ceil(log2(max(amax|n|, 1e-4)/448)),
+//      scale byte e + 127, code = e4m3_rne(n / 2^e);
+//   4. codes of kept coordinates in ascending order, MSB-first bitmap words.
+#include "remnant_device.h"
+#include "remnant_mi355x.h"
+
+using namespace rm;
+
+namespace {
+
+constexpr int kWaves = 4;
+
+template <bool kBf16>
+__device__ __forceinline__ void load_row8(const void* x, int64_t row, int64_t stride,
+                                          int lane, float* v) {
+  if (kBf16) {
+    const uint16_t* p = (const uint16_t*)x + row * stride + 8 * lane;
+    u32x4 d = *(const u32x4*)p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = u2f(d[i] << 16);
+      v[2 * i + 1] = u2f(d[i] & 0xffff0000u);
+    }
+  } else {
+    const float* p = (const float*)x + row * stride + 8 * lane;
+    f32x4 a = *(const f32x4*)p, b = *(const f32x4*)(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[4 + i] = b[i];
+    }
+  }
+}
+
+// Sum over the wave in the fixed pairwise order (distance 1, 2, ..., 32).
+__device__ __forceinline__ float wave_tree_sum(float p) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) p = p + __shfl_xor(p, d, 64);
+  return p;
+}
+
+__device__ __forceinline__ int popc_ballot(bool pred) {
+  return __popcll(__ballot(pred));
+}
+
+// Exclusive count of set predicates in lanes below this one.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// Keep mask (bit i = coordinate 8*lane + i) of the 256 largest magnitudes.
+template <bool kBf16>
+__device__ __forceinline__ uint32_t select_top256(const uint32_t* key) {
+  constexpr int kLow = kBf16 ? 16 : 0;  // bf16 magnitudes have zero low halves
+  uint32_t prefix = 0;
+  bool exact = false;
+  for (int b = 30; b >= kLow; --b) {
+    uint32_t cand = prefix | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cnt += popc_ballot(key[i] >= cand);
+    if (cnt >= kKeep) prefix = cand;
+    if (cnt == kKeep) {  // {key >= cand} is exactly the top 256: no boundary tie
+      exact = true;
+      break;
+    }
+  }
+  uint32_t keep = 0;
+  if (exact) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) keep |= (key[i] >= prefix ? 1u : 0u) << i;
+    return keep;
+  }
+  // prefix is the 256th largest key; admit ties at it in coordinate order.
+  int gt = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) gt += popc_ballot(key[i] > prefix);
+  int need = kKeep - gt;
+  int before = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) before += lanes_below(__ballot(key[i] == prefix));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    bool tie = key[i] == prefix;
+    bool k = key[i] > prefix || (tie && before < need);
+    before += tie ? 1 : 0;
+    keep |= (k ? 1u : 0u) << i;
+  }
+  return keep;
+}
+
+template <bool kBf16>
+__global__ __launch_bounds__(256) void pack_rows_kernel(
+    const void* __restrict__ x, int64_t stride, const float* __restrict__ weight, float eps,
+    const int32_t* __restrict__ slots, int64_t n, uint8_t* __restrict__ pool,
+    int64_t pool_rows) {
+  __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][336];
+  const int lane = wave_lane();
+  const int wave = uniform((int)(threadIdx.x >> 6));
+  uint8_t* st = stage[wave];
+  float w[8];
+  {
+    f32x4 a = *(const f32x4*)(weight + 8 * lane), b = *(const f32x4*)(weight + 8 * lane + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = a[i];
+      w[4 + i] = b[i];
+    }
+  }
+  for (int64_t rec = (int64_t)blockIdx.x * kWaves + wave; rec < n;
+       rec += (int64_t)gridDim.x * kWaves) {
+    const int64_t slot = slots[rec];
+    if (slot < 0 || slot >= pool_rows) continue;
+    float v[8];
+    uint32_t key[8];
+    load_row8<kBf16>(x, rec, stride, lane, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) key[i] = f2u(v[i]) & 0x7fffffffu;
+    const uint32_t keep = select_top256<kBf16>(key);
+
+    // masked RMSNorm
+    float m[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m[i] = (keep >> i) & 1u ? v[i] : 0.0f;
+    float p = m[0] * m[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+      float sq = m[i] * m[i];
+      p = p + sq;
+    }
+    const float sumsq = wave_tree_sum(p);
+    const float r = __fdiv_rn(1.0f, __fsqrt_rn(sumsq * (1.0f / 512.0f) + eps));
+    uint32_t nb[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float y = m[i] * r;
+      y = y * w[i];
+      nb[i] = bf16_rne(y);
+      amax = fmaxf(amax, fabsf(bf16_to_f32(nb[i])));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    const int e = ue8m0_exponent(amax);
+    const float inv = exp2i(-e);
+
+    // compaction: rank of this lane's first survivor among all survivors
+    int rank = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rank += lanes_below(__ballot((keep >> i) & 1u));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if ((keep >> i) & 1u) {
+        st[rank] = (uint8_t)e4m3_rne(bf16_to_f32(nb[i]) * inv);
+        ++rank;
+      }
+    }
+    // bitmap byte: coordinate 8l+i is bit 7-i of byte 7 - l%8 of word l/8
+    const uint32_t rev = __builtin_bitreverse32(keep) >> 24;
+    st[kCodeBytes + 8 * (lane >> 3) + 7 - (lane & 7)] = (uint8_t)rev;
+    if ((lane & 7) == 0) st[kDataBytes + (lane >> 3)] = (uint8_t)(e + 127);
+    wave_lds_sync();
+
+    uint8_t* page = pool + (slot >> 6) * kPageBytes;
+    const int row = (int)(slot & 63);
+    if (lane < kDataBytes / 16) {
+      *(u32x4*)(page + row * kDataBytes + 16 * lane) = *(const u32x4*)(st + 16 * lane);
+    } else if (lane == kDataBytes / 16) {
+      *(u32x2*)(page + kPageRecords * kDataBytes + row * kScaleBytes) =
+          *(const u32x2*)(st + kDataBytes);
+    }
+    wave_lds_sync();
+  }
+}
+
+template <bool kBf16>
+__global__ __launch_bounds__(256) void native_store_kernel(
+    const void* __restrict__ x, int64_t stride, const float* __restrict__ weight, float eps,
+    const int32_t* __restrict__ slots, const int32_t* __restrict__ position,
+    const float* __restrict__ freqs, int64_t freq_rows, int64_t n, uint8_t* __restrict__ pool,
+    int64_t pool_rows) {
+  const int lane = wave_lane();
+  const int wave = uniform((int)(threadIdx.x >> 6));
+  float w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w[i] = weight[8 * lane + i];
+  for (int64_t rec = (int64_t)blockIdx.x * kWaves + wave; rec < n;
+       rec += (int64_t)gridDim.x * kWaves) {
+    const int64_t slot = slots[rec];
+    if (slot < 0 || slot >= pool_rows) continue;
+    int64_t pos = 0;
+    if (freqs) {
+      pos = position[rec];
+      if (pos < 0 || pos * 4 >= freq_rows) continue;
+    }
+    float v[8];
+    load_row8<kBf16>(x, rec, stride, lane, v);
+    float p = v[0] * v[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+      float sq = v[i] * v[i];
+      p = p + sq;
+    }
+    const float sumsq = wave_tree_sum(p);
+    const float r = __fdiv_rn(1.0f, __fsqrt_rn(sumsq * (1.0f / 512.0f) + eps));
+    float nf[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float y = v[i] * r;
+      y = y * w[i];
+      nf[i] = bf16_to_f32(bf16_rne(y));
+      amax = fmaxf(amax, fabsf(nf[i]));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    uint8_t* page = pool + (slot >> 6) * kNativePageBytes;
+    const int row = (int)(slot & 63);
+    uint8_t* data = page + row * kNativeDataBytes;
+    if (lane < kNopeDim / 8) {
+      const int e = ue8m0_exponent(amax);
+      const float inv = exp2i(-e);
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lo |= e4m3_rne(nf[i] * inv) << (8 * i);
+        hi |= e4m3_rne(nf[4 + i] * inv) << (8 * i);
+      }
+      *(u32x2*)(data + 8 * lane) = u32x2{lo, hi};
+      uint8_t* srow = page + kPageRecords * kNativeDataBytes + row * kScaleBytes;
+      if ((lane & 7) == 0) srow[lane >> 3] = (uint8_t)(e + 127);
+      if (lane == 0) srow[7] = 0;
+    } else {
+      if (freqs) {
+        const float* f = freqs + (pos * 4) * (2 * kRopePairs) + 8 * (lane - kNopeDim / 8);
+        float cs[8];
+        f32x4 a = *(const f32x4*)f, b = *(const f32x4*)(f + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          cs[i] = a[i];
+          cs[4 + i] = b[i];
+        }
+        rope4(nf, cs);
+      }
+      u32x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = bf16_rne(nf[2 * i]) | (bf16_rne(nf[2 * i + 1]) << 16);
+      *(u32x4*)(data + kNopeDim + 16 * (lane - kNopeDim / 8)) = o;
+    }
+  }
+}
+
+int grid_for(int64_t n) {
+  int64_t blocks = (n + kWaves - 1) / kWaves;
+  const int64_t cap = 256 * 32;  // 256 CUs x 32 resident waves' worth of blocks
+  return (int)(blocks < cap ? blocks : cap);
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+}  // namespace
+
+extern "C" int rm_pack_rows(const void* x, int x_dtype, int64_t x_row_stride,
+                            const float* weight, float eps, const int32_t* dst_slot, int64_t n,
+                            uint8_t* pool, int64_t pool_pages, void* stream) {
+  if (n < 0 || pool_pages < 0) return RM_ERR_SHAPE;
+  if (n == 0) return RM_OK;
+  if (!x || !weight || !dst_slot || !pool) return RM_ERR_NULL;
+  if (x_dtype != RM_F32 && x_dtype != RM_BF16) return RM_ERR_DTYPE;
+  if (x_row_stride < kHeadDim && n > 1) return RM_ERR_SHAPE;
+  const int esize = x_dtype == RM_BF16 ? 2 : 4;
+  if (!aligned(x, 16) || ((x_row_stride * esize) & 15) || !aligned(weight, 16) ||
+      !aligned(pool, 16))
+    return RM_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t rows = pool_pages * kPageRecords;
+  if (x_dtype == RM_BF16)
+    hipLaunchKernelGGL(pack_rows_kernel<true>, dim3(grid_for(n)), dim3(256), 0, s, x,
+                       x_row_stride, weight, eps, dst_slot, n, pool, rows);
+  else
+    hipLaunchKernelGGL(pack_rows_kernel<false>, dim3(grid_for(n)), dim3(256), 0, s, x,
+                       x_row_stride, weight, eps, dst_slot, n, pool, rows);
+  return hipGetLastError() == hipSuccess ? RM_OK : RM_ERR_LAUNCH;
+}
+
+extern "C" int rm_native_store_rows(const void* x, int x_dtype, int64_t x_row_stride,
+                                    const float* weight, float eps, const int32_t* dst_slot,
+                                    const int32_t* position, const float* freqs,
+                                    int64_t freq_rows, int64_t n, uint8_t* pool,
+                                    int64_t pool_pages, void* stream) {
+  if (n < 0 || pool_pages < 0 || freq_rows < 0) return RM_ERR_SHAPE;
+  if (n == 0) return RM_OK;
+  if (!x || !weight || !dst_slot || !pool || (freqs && !position)) return RM_ERR_NULL;
+  if (x_dtype != RM_F32 && x_dtype != RM_BF16) return RM_ERR_DTYPE;
+  if (x_row_stride < kHeadDim && n > 1) return RM_ERR_SHAPE;
+  const int esize = x_dtype == RM_BF16 ? 2 : 4;
+  if (!aligned(x, 16) || ((x_row_stride * esize) & 15) || !aligned(pool, 16) ||
+      (freqs && !aligned(freqs, 16)))
+    return RM_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t rows = pool_pages * kPageRecords;
+  if (x_dtype == RM_BF16)
+    hipLaunchKernelGGL(native_store_kernel<true>, dim3(grid_for(n)), dim3(256), 0, s, x,
+                       x_row_stride, weight, eps, dst_slot, position, freqs, freq_rows, n,
+                       pool, rows);
+  else
+    hipLaunchKernelGGL(native_store_kernel<false>, dim3(grid_for(n)), dim3(256), 0, s, x,
+                       x_row_stride, weight, eps, dst_slot, position, freqs, freq_rows, n,
+                       pool, rows);
+  return hipGetLastError() == hipSuccess ? RM_OK : RM_ERR_LAUNCH;
+}

@@ -1,0 +1,167 @@
+"""Packed store and reconstruct operators (torch tensors in, HIP kernels out).
+
+Host-side mirror of the reference's fork ``srt/remnant/packed.py``:
+``pack_rows_fused`` (fused Triton store, third_party/README.md:257) and
+``unpack_gather_bf16`` (candidate-sglang.patch:427-480): same names, argument
+meaning, ``ValueError``/``TypeError`` behaviour and empty-input rule (return
+``output`` untouched, launch nothing). Work runs on the current HIP stream,
+asynchronously, through the C ABI in include/remnant_mi355x.h.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib, config
+from .pool import LatentPool
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _as_pool(buffers, layer_id) -> tuple[torch.Tensor, bool]:
+    """Resolve a LatentPool (+ layer) or a raw uint8 page tensor [pages, page_bytes]."""
+    if isinstance(buffers, LatentPool):
+        return buffers.layer(layer_id), buffers.packed
+    if isinstance(buffers, torch.Tensor):
+        if buffers.dtype != torch.uint8 or buffers.dim() != 2 or not buffers.is_contiguous():
+            raise ValueError("pool must be a contiguous uint8 [pages, page_bytes] tensor")
+        if buffers.shape[1] == config.PACKED_PAGE_BYTES:
+            return buffers, True
+        if buffers.shape[1] == config.NATIVE_PAGE_BYTES:
+            return buffers, False
+        raise ValueError(f"unknown page size {buffers.shape[1]}")
+    raise ValueError("packed_buffers must be a LatentPool or a uint8 page tensor")
+
+
+def _check_cuda(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("tensors must live on the GPU")
+
+
+def pack_rows_fused(x: torch.Tensor, weight: torch.Tensor, eps: float, loc: torch.Tensor,
+                    pool, *, layer_id: int | None = None) -> None:
+    """Pack raw C4 rows ``x`` [n, 512] (float32 compressor output or bfloat16)
+    into Packed records at pool slots ``loc`` [n] int32 (slots outside the
+    pool are skipped)."""
+    buf, packed = _as_pool(pool, layer_id)
+    if not packed:
+        raise ValueError("pack_rows_fused writes the Packed (remnant) format")
+    if x.dim() != 2 or x.shape[-1] != config.HEAD_DIM or x.stride(-1) != 1:
+        raise ValueError("x must be [rows, 512] with unit inner stride")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("x must be float32 or bfloat16")
+    if loc.dtype != torch.int32 or loc.shape != (x.shape[0],) or not loc.is_contiguous():
+        raise ValueError("loc must be a contiguous int32 [rows] tensor")
+    if weight.dtype != torch.float32 or weight.shape != (config.HEAD_DIM,) or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous float32 [512] tensor")
+    if x.shape[0] == 0:
+        return
+    _check_cuda(x, weight, loc, buf)
+    dtype = 1 if x.dtype == torch.bfloat16 else 0
+    _lib.check(_lib.load().rm_pack_rows(
+        x.data_ptr(), dtype, x.stride(0), weight.data_ptr(), float(eps), loc.data_ptr(),
+        x.shape[0], buf.data_ptr(), buf.shape[0], _stream()), "rm_pack_rows")
+
+
+def native_store_rows(x: torch.Tensor, weight: torch.Tensor, eps: float, loc: torch.Tensor,
+                      positions: torch.Tensor | None, freqs_cis: torch.Tensor | None, pool,
+                      *, layer_id: int | None = None) -> None:
+    """Native 584-byte control store (unpruned RMSNorm, tail rotated with
+    frequency row positions * 4)."""
+    buf, packed = _as_pool(pool, layer_id)
+    if packed:
+        raise ValueError("native_store_rows writes the Native format")
+    if x.dim() != 2 or x.shape[-1] != config.HEAD_DIM or x.stride(-1) != 1:
+        raise ValueError("x must be [rows, 512] with unit inner stride")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("x must be float32 or bfloat16")
+    if loc.dtype != torch.int32 or loc.shape != (x.shape[0],) or not loc.is_contiguous():
+        raise ValueError("loc must be a contiguous int32 [rows] tensor")
+    freq_ptr, freq_rows, pos_ptr = None, 0, None
+    if freqs_cis is not None:
+        if not freqs_cis.is_complex() or not freqs_cis.is_contiguous():
+            raise ValueError("freqs_cis must be a contiguous complex tensor")
+        if positions is None or positions.dtype != torch.int32 or positions.shape != loc.shape:
+            raise ValueError("positions must be int32 [rows] when freqs_cis is given")
+        freq_ptr = freqs_cis.data_ptr()
+        freq_rows = freqs_cis.numel() // (config.ROPE_DIM // 2)
+        pos_ptr = positions.contiguous().data_ptr()
+    if x.shape[0] == 0:
+        return
+    _check_cuda(x, weight, loc, buf, freqs_cis)
+    dtype = 1 if x.dtype == torch.bfloat16 else 0
+    _lib.check(_lib.load().rm_native_store_rows(
+        x.data_ptr(), dtype, x.stride(0), weight.contiguous().data_ptr(), float(eps),
+        loc.data_ptr(), pos_ptr, freq_ptr, freq_rows, x.shape[0], buf.data_ptr(),
+        buf.shape[0], _stream()), "rm_native_store_rows")
+
+
+def unpack_gather_bf16(packed_buffers, physical_indices: torch.Tensor,
+                       raw_indices: torch.Tensor | None, topk_lengths: torch.Tensor,
+                       freqs_cis: torch.Tensor | None, output: torch.Tensor, *,
+                       layer_id: int | None = None, fused_rope: bool = False) -> torch.Tensor:
+    """Gather selected records, dequantize, zero-fill and apply tail RoPE.
+
+    physical/raw indices are int32 [queries, k] (any strides); physical entries
+    address pool slots, raw entries logical C4 rows (frequency row raw * 4).
+    Lengths are int32 [queries]. ``output`` is caller-owned contiguous BF16 with
+    at least queries * k rows of 512. Invalid/padded selections produce zero
+    rows. ``freqs_cis=None`` returns pre-RoPE rows. The MI355X kernel always
+    reads in one pass and rounds dequantized values to BF16 before rotating, so
+    ``fused_rope`` True and False give the same bytes (the reference requires
+    its fused and split readers to agree bitwise, candidate-sglang.patch:682-686).
+    """
+    if type(fused_rope) is not bool:
+        raise TypeError("fused_rope must be a bool")
+    buf, packed = _as_pool(packed_buffers, layer_id)
+    if not packed:
+        raise ValueError("unpack_gather_bf16 reads the Packed (remnant) format")
+    if raw_indices is not None and physical_indices.shape != raw_indices.shape:
+        raise ValueError("physical_indices and raw_indices must have equal shape")
+    if physical_indices.dim() != 2:
+        raise ValueError("indices must be [queries, k]")
+    for name, t in (("physical_indices", physical_indices), ("raw_indices", raw_indices),
+                    ("topk_lengths", topk_lengths)):
+        if t is not None and t.dtype != torch.int32:
+            raise ValueError(f"{name} must be int32")
+    n_queries, selected_k = physical_indices.shape
+    if topk_lengths.dim() != 1 or topk_lengths.shape[0] != n_queries:
+        raise ValueError("topk_lengths must be [queries]")
+    if output.dtype != torch.bfloat16 or not output.is_contiguous() or output.dim() != 2 \
+            or output.shape[-1] != config.HEAD_DIM:
+        raise ValueError("output must be a contiguous bfloat16 [rows, 512] tensor")
+    if output.shape[0] < n_queries * selected_k:
+        raise ValueError("output has fewer rows than queries * k")
+    freq_ptr, freq_rows = None, 0
+    if freqs_cis is not None:
+        if not freqs_cis.is_complex() or not freqs_cis.is_contiguous():
+            raise ValueError("freqs_cis must be a contiguous complex tensor")
+        if freqs_cis.dtype != torch.complex64:
+            raise ValueError("freqs_cis must be complex64")
+        if raw_indices is None:
+            raise ValueError("raw_indices are required with freqs_cis")
+        freq_ptr = freqs_cis.data_ptr()
+        freq_rows = freqs_cis.numel() // (config.ROPE_DIM // 2)
+    if n_queries * selected_k == 0:
+        return output
+    _check_cuda(buf, physical_indices, raw_indices, topk_lengths, output, freqs_cis)
+    _lib.check(_lib.load().rm_unpack_gather_bf16(
+        buf.data_ptr(), buf.shape[0], physical_indices.data_ptr(), physical_indices.stride(0),
+        physical_indices.stride(1), None if raw_indices is None else raw_indices.data_ptr(),
+        0 if raw_indices is None else raw_indices.stride(0),
+        0 if raw_indices is None else raw_indices.stride(1), topk_lengths.data_ptr(),
+        topk_lengths.stride(0), n_queries, selected_k, freq_ptr, freq_rows, output.data_ptr(),
+        _stream()), "rm_unpack_gather_bf16")
+    return output
+
+
+def unpack_rows(pool, slots: torch.Tensor, *, layer_id: int | None = None) -> torch.Tensor:
+    """Pre-RoPE BF16 rows [n, 512] of pool slots (exact dequantization)."""
+    slots = slots.to(torch.int32).reshape(1, -1).contiguous()
+    out = torch.empty((slots.shape[1], config.HEAD_DIM), dtype=torch.bfloat16,
+                      device=slots.device)
+    lengths = torch.full((1,), slots.shape[1], dtype=torch.int32, device=slots.device)
+    return unpack_gather_bf16(pool, slots, None, lengths, None, out, layer_id=layer_id)

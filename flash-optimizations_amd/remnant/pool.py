@@ -1,0 +1,92 @@
+"""Paged C4 latent pool (per-layer planes in HBM).
+
+Reference: fork ``srt/mem_cache/deepseek_v4_memory_pool.py`` allocates per-layer
+Packed planes ``values`` u8 [rows, 256], ``bitmaps`` u64 [rows, 8] and
+``scales`` u8 [rows, 8] (candidate-sglang.patch:900-904) in pages of 64 C4
+records (decode-store timing.json ``page_size: 64``).
+
+MI355X layout: one contiguous uint8 buffer [layers, pages, page_bytes]. A page
+keeps its 64 data rows (codes + bitmap, 320 B each, every row 16-byte aligned)
+followed by its 64 scale rows (8 B), so a record's hot bytes are one aligned
+320-byte span for 16-byte vector loads. The three reference planes are exposed
+as strided views of the same memory (no copies), which is what a host-cache
+transfer or an inspection needs.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import config
+
+
+class LatentPool:
+    def __init__(self, pages: int, layers: int = 1, fmt: str = "remnant", device="cuda"):
+        if fmt == "direct":
+            fmt = "remnant"
+        if fmt not in ("remnant", "native"):
+            raise ValueError(f"unsupported cache format: {fmt!r}")
+        if pages < 0 or layers < 1:
+            raise ValueError("pages must be >= 0 and layers >= 1")
+        self.fmt = fmt
+        self.pages = pages
+        self.layers = layers
+        self.page_bytes = config.PACKED_PAGE_BYTES if fmt == "remnant" else config.NATIVE_PAGE_BYTES
+        self.data_bytes = config.PACKED_DATA_BYTES if fmt == "remnant" else config.NATIVE_DATA_BYTES
+        self.buffer = torch.zeros((layers, pages, self.page_bytes), dtype=torch.uint8,
+                                  device=device)
+
+    @property
+    def packed(self) -> bool:
+        return self.fmt == "remnant"
+
+    @property
+    def rows(self) -> int:
+        return self.pages * config.PAGE_RECORDS
+
+    @property
+    def record_bytes(self) -> int:
+        return self.data_bytes + 8
+
+    def layer(self, layer_id: int | None = None) -> torch.Tensor:
+        return self.buffer[0 if layer_id is None else layer_id]
+
+    def _data_rows(self, layer_id):
+        pg = self.layer(layer_id)[:, : config.PAGE_RECORDS * self.data_bytes]
+        return pg.reshape(self.pages, config.PAGE_RECORDS, self.data_bytes)
+
+    def scales(self, layer_id: int | None = None) -> torch.Tensor:
+        """Scale plane view [pages, 64, 8] u8."""
+        pg = self.layer(layer_id)[:, config.PAGE_RECORDS * self.data_bytes:]
+        return pg.reshape(self.pages, config.PAGE_RECORDS, 8)
+
+    def values(self, layer_id: int | None = None) -> torch.Tensor:
+        """Code plane view: Packed [pages, 64, 256] u8, Native [pages, 64, 448] u8."""
+        width = config.KEEP_COUNT if self.packed else config.NOPE_DIM
+        return self._data_rows(layer_id)[..., :width]
+
+    def bitmaps(self, layer_id: int | None = None) -> torch.Tensor:
+        """Bitmap plane view [pages, 64, 64] u8 (8 little-endian MSB-first uint64 words)."""
+        if not self.packed:
+            raise ValueError("Native records carry no bitmap")
+        return self._data_rows(layer_id)[..., config.KEEP_COUNT:config.PACKED_DATA_BYTES]
+
+    def records(self, slots: torch.Tensor, layer_id: int | None = None) -> torch.Tensor:
+        """Logical records [n, record_bytes] (data row + scale row) for pool slots."""
+        slots = slots.to(torch.long)
+        page, row = slots // config.PAGE_RECORDS, slots % config.PAGE_RECORDS
+        data = self._data_rows(layer_id)[page, row]
+        return torch.cat([data, self.scales(layer_id)[page, row]], dim=-1)
+
+    def capacity_records(self) -> int:
+        return self.rows
+
+    def nbytes(self) -> int:
+        return self.buffer.numel()
+
+
+def records_fitting(nbytes: int, fmt: str = "remnant") -> int:
+    """Whole pages of records that fit in ``nbytes`` of HBM."""
+    fmt = "remnant" if fmt == "direct" else fmt
+    page = config.PACKED_PAGE_BYTES if fmt == "remnant" else config.NATIVE_PAGE_BYTES
+    return (nbytes // page) * config.PAGE_RECORDS

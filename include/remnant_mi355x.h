@@ -1,0 +1,148 @@
+/*
+ * remnant_mi355x.h -- C ABI of the MI355X (gfx950) Remnant packed-KV hot path.
+ *
+ * Plain pointers and sizes only: device pointers for tensors, a hipStream_t
+ * passed as void*. Every entry point is asynchronous on the given stream,
+ * allocates nothing, and returns an rm_status (0 = ok, negative = rejected
+ * argument; nothing was launched). Empty inputs return RM_OK without a launch.
+ *
+ * Pool geometry (identical for every entry point):
+ *   Packed page (20,992 B) = 64 data rows of 320 B (256 E4M3 codes in ascending
+ *   coordinate order, then 8 little-endian uint64 bitmap words, MSB-first:
+ *   coordinate c is bit 63 - c % 64 of word c / 64) followed by 64 scale rows
+ *   of 8 UE8M0 bytes. Logical record size 328 B.
+ *   Native page (37,376 B) = 64 data rows of 576 B (448 E4M3 codes, 64 rotated
+ *   BF16) followed by 64 scale rows (7 UE8M0 bytes + 1 zero byte). 584 B/record.
+ *   Pool slot s lives in page s / 64, row s % 64.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   rm_pack_rows              fork srt/remnant/packed.py::pack_rows_fused and the
+ *                             fused Triton store (third_party/README.md:257,
+ *                             378-381; called from compressor_v2.py store dispatch)
+ *   rm_native_store_rows      stock fused_norm_rope_flashmla store (Native control;
+ *                             decode-store manifest.json source.native_store)
+ *   rm_unpack_gather_bf16     srt/remnant/packed.py::unpack_gather_bf16
+ *                             (benchmarks/microbench/dsv4-flash-prefill-read-fused-rope/
+ *                             candidate-sglang.patch:427-480, kernels :502-668)
+ *   rm_remnant_sparse_decode_fwd
+ *                             sgl_kernel/flash_mla.py::remnant_sparse_decode_fwd,
+ *                             FlashMLA csrc/api/sparse_decode.h Direct decode +
+ *                             combine (third_party/README.md:260, 351-361;
+ *                             Dockerfile.v0.5.18:56-57)
+ *   rm_native_sparse_decode_fwd
+ *                             stock FlashMLA sparse FP8 decode on 584-B records
+ *                             (Native control, same harness)
+ *   rm_sparse_decode_workspace  FlashMLA get_mla_metadata-style split planning
+ */
+#ifndef REMNANT_MI355X_H
+#define REMNANT_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum rm_status {
+  RM_OK = 0,
+  RM_ERR_NULL = -1,      /* required pointer missing */
+  RM_ERR_SHAPE = -2,     /* size/stride out of range */
+  RM_ERR_ALIGN = -3,     /* pointer not aligned as documented */
+  RM_ERR_DTYPE = -4,     /* unsupported dtype code */
+  RM_ERR_WORKSPACE = -5, /* workspace too small */
+  RM_ERR_LAUNCH = -6     /* the HIP runtime rejected the launch */
+};
+
+enum rm_dtype { RM_F32 = 0, RM_BF16 = 1 };
+
+#define RM_HEAD_DIM 512
+#define RM_NOPE_DIM 448
+#define RM_ROPE_PAIRS 32
+#define RM_KEEP_COUNT 256
+#define RM_PAGE_RECORDS 64
+#define RM_PACKED_DATA_BYTES 320
+#define RM_PACKED_RECORD_BYTES 328
+#define RM_PACKED_PAGE_BYTES 20992
+#define RM_NATIVE_DATA_BYTES 576
+#define RM_NATIVE_RECORD_BYTES 584
+#define RM_NATIVE_PAGE_BYTES 37376
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int rm_version(void);
+
+/* Store: pack n latent rows into Packed records.
+ * x: [n, 512] with row stride x_row_stride elements, dtype RM_F32 or RM_BF16
+ *    (raw compressor output; 16-byte aligned rows).
+ * weight: [512] f32 RMSNorm weight. eps: RMSNorm epsilon.
+ * dst_slot: [n] int32 pool slots; a slot < 0 or >= pool_pages * 64 is skipped.
+ * pool: packed pages (16-byte aligned). */
+int rm_pack_rows(const void* x, int x_dtype, int64_t x_row_stride, const float* weight,
+                 float eps, const int32_t* dst_slot, int64_t n, uint8_t* pool,
+                 int64_t pool_pages, void* stream);
+
+/* Native control store: unpruned RMSNorm, 7 NoPE groups as UE8M0/E4M3, tail
+ * rotated with freqs row position[i] * 4 (freqs: [freq_rows, 32] complex64 as
+ * interleaved f32 (cos, sin); NULL = no rotation). Rows whose slot is out of
+ * range, or (with freqs) whose position * 4 is outside [0, freq_rows), are skipped. */
+int rm_native_store_rows(const void* x, int x_dtype, int64_t x_row_stride,
+                         const float* weight, float eps, const int32_t* dst_slot,
+                         const int32_t* position, const float* freqs, int64_t freq_rows,
+                         int64_t n, uint8_t* pool, int64_t pool_pages, void* stream);
+
+/* Reconstruct: out row (q, k) (row index q * selected_k + k, 512 BF16 values,
+ * contiguous) = dequantized record physical[q, k], tail rotated by freqs row
+ * raw[q, k] * 4. A row is zero unless k < lengths[q], 0 <= physical < pool rows
+ * and (with freqs) 0 <= raw * 4 < freq_rows. freqs == NULL selects the pre-RoPE
+ * reader (raw may be NULL). Strides are in int32 elements. */
+int rm_unpack_gather_bf16(const uint8_t* pool, int64_t pool_pages, const int32_t* physical,
+                          int64_t physical_stride_q, int64_t physical_stride_k,
+                          const int32_t* raw, int64_t raw_stride_q, int64_t raw_stride_k,
+                          const int32_t* lengths, int64_t length_stride, int64_t n_queries,
+                          int64_t selected_k, const float* freqs, int64_t freq_rows,
+                          uint16_t* out, void* stream);
+
+/* Split planning for the sparse decode of `tokens` query tokens with `topk`
+ * selected records each and `heads` query heads. Writes the number of split-KV
+ * partitions and the workspace bytes the decode needs (0 when no split). */
+int rm_sparse_decode_workspace(int64_t tokens, int64_t heads, int64_t topk,
+                               int32_t* num_splits, size_t* workspace_bytes);
+
+/* Direct packed sparse-MLA decode.
+ * q: [batch * q_len, heads, 512] BF16, contiguous; heads a multiple of 16.
+ * pool: packed pages. block_table: [batch, block_table_stride] int32; logical
+ * record r of request b is pool slot block_table[b, r / 64] * 64 + r % 64.
+ * max_blocks: valid columns of the block table. seqlens: [batch] int32 records
+ * per request (NULL = unbounded). indices: [batch * q_len, topk] int32 logical
+ * records (-1 = padding). topk_length: [batch * q_len] int32 (NULL = topk).
+ * sink: [heads] f32 logits (NULL = no sink). freqs/freq_rows: RoPE table for
+ * the stored pre-RoPE tail, row = record * 4 (NULL = tail used as stored).
+ * Output: out [batch * q_len, heads, 512] BF16; lse [batch * q_len, heads] f32,
+ * natural log of sum_j exp(l_j) + exp(sink). Invalid entries (k >= length,
+ * r < 0, r >= seqlen, unmapped block, row beyond the table) contribute nothing.
+ * workspace: rm_sparse_decode_workspace bytes (may be NULL when it reports 0). */
+int rm_remnant_sparse_decode_fwd(const uint16_t* q, int64_t batch, int64_t q_len,
+                                 int64_t heads, const uint8_t* pool, int64_t pool_pages,
+                                 const int32_t* block_table, int64_t block_table_stride,
+                                 int64_t max_blocks, const int32_t* seqlens,
+                                 const int32_t* indices, int64_t topk,
+                                 const int32_t* topk_length, const float* sink,
+                                 const float* freqs, int64_t freq_rows, float softmax_scale,
+                                 uint16_t* out, float* lse, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* Native control decode: same contract on 584-byte records (tail already rotated). */
+int rm_native_sparse_decode_fwd(const uint16_t* q, int64_t batch, int64_t q_len,
+                                int64_t heads, const uint8_t* pool, int64_t pool_pages,
+                                const int32_t* block_table, int64_t block_table_stride,
+                                int64_t max_blocks, const int32_t* seqlens,
+                                const int32_t* indices, int64_t topk,
+                                const int32_t* topk_length, const float* sink,
+                                float softmax_scale, uint16_t* out, float* lse,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* REMNANT_MI355X_H */

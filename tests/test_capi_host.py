@@ -1,0 +1,188 @@
+"""CPU tests of the boundary: the C-ABI library loads and exports every symbol
+include/remnant_mi355x.h declares, rejects bad arguments with the documented
+status codes before touching the GPU, and the Python host layer mirrors the
+reference's validation and empty-input behaviour (candidate-sglang.patch:
+435-453, 918-930). No kernel is launched here."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import remnant
+from remnant import _lib, config
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "remnant_mi355x.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*int\s+(rm_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 7
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES)
+    assert lib.rm_version() >= 100
+
+
+def test_header_geometry_matches_python_config():
+    text = open(HEADER).read()
+    consts = dict(re.findall(r"#define (RM_\w+) (\d+)", text))
+    assert int(consts["RM_PACKED_RECORD_BYTES"]) == config.PACKED_RECORD_BYTES == 328
+    assert int(consts["RM_NATIVE_RECORD_BYTES"]) == config.NATIVE_RECORD_BYTES == 584
+    assert int(consts["RM_PACKED_PAGE_BYTES"]) == config.PACKED_PAGE_BYTES == 64 * 328
+    assert int(consts["RM_NATIVE_PAGE_BYTES"]) == config.NATIVE_PAGE_BYTES == 64 * 584
+    assert int(consts["RM_KEEP_COUNT"]) + 64 + 8 == 328
+
+
+def buf(n=64, align=256):
+    raw = ctypes.create_string_buffer(n + align)
+    addr = ctypes.addressof(raw)
+    return raw, addr + (-addr % align)
+
+
+def test_capi_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    keep = []
+    _, x = buf(4096)
+    _, w = buf(2048)
+    _, s = buf(64)
+    _, pool = buf(21000)
+    keep += [x, w, s, pool]
+    assert lib.rm_pack_rows(x, 1, 512, w, 1e-6, s, 0, pool, 1, None) == 0  # empty: no launch
+    assert lib.rm_pack_rows(x, 1, 512, w, 1e-6, s, -1, pool, 1, None) == -2
+    assert lib.rm_pack_rows(None, 1, 512, w, 1e-6, s, 4, pool, 1, None) == -1
+    assert lib.rm_pack_rows(x, 7, 512, w, 1e-6, s, 4, pool, 1, None) == -4
+    assert lib.rm_pack_rows(x + 2, 1, 512, w, 1e-6, s, 4, pool, 1, None) == -3
+    assert lib.rm_pack_rows(x, 1, 100, w, 1e-6, s, 4, pool, 1, None) == -2
+    assert lib.rm_native_store_rows(x, 0, 512, w, 1e-6, s, None, w, 8, 4, pool, 1, None) == -1
+    assert lib.rm_unpack_gather_bf16(pool, 1, s, 1, 1, None, 0, 0, s, 1, 0, 5, None, 0, x,
+                                     None) == 0
+    assert lib.rm_unpack_gather_bf16(pool, 1, s, 1, 1, None, 0, 0, s, 1, 2, 5, w, 8, x,
+                                     None) == -1  # freqs without raw
+    assert lib.rm_unpack_gather_bf16(pool, 1, s, 1, 1, None, 0, 0, s, 1, 2, 5, None, 0, x + 8,
+                                     None) == -3
+    args = [x, 1, 1, 17, pool, 1, s, 4, 4, None, s, 8, None, None, None, 0, 0.1, x, w, None, 0,
+            None]
+    assert lib.rm_remnant_sparse_decode_fwd(*args) == -2  # 17 heads
+    args[3] = 16
+    args[8] = 9  # max_blocks beyond the table stride
+    assert lib.rm_remnant_sparse_decode_fwd(*args) == -2
+    args[8] = 4
+    args[11] = 64  # top-k 64 at batch 1 plans 4 splits
+    assert lib.rm_remnant_sparse_decode_fwd(*args) == -5  # split plan needs a workspace
+    assert lib.rm_native_sparse_decode_fwd(x, 0, 1, 16, pool, 1, s, 4, 4, None, s, 8, None,
+                                           None, 0.1, x, w, None, 0, None) == 0
+
+
+def test_decode_split_plan():
+    for tokens, topk in ((1, 2048), (64, 2048), (256, 2048), (3, 10), (1000, 16)):
+        splits, nbytes = remnant.get_decode_metadata(tokens, 16, topk)
+        assert 1 <= splits <= max(1, -(-topk // 16))
+        assert nbytes == (0 if splits == 1 else tokens * splits * 16 * 513 * 4)
+    assert remnant.get_decode_metadata(1, 16, 2048)[0] > 1  # batch 1 spreads over CUs
+    with pytest.raises(RuntimeError):
+        remnant.get_decode_metadata(1, 17, 64)
+
+
+def test_unpack_gather_host_validation_mirrors_reference():
+    pool = torch.zeros((1, config.PACKED_PAGE_BYTES), dtype=torch.uint8)
+    index = torch.zeros((1, 1), dtype=torch.int32)
+    lengths = torch.ones(1, dtype=torch.int32)
+    freqs = torch.ones((16, 32), dtype=torch.complex64)
+    output = torch.full((1, 512), -91.0, dtype=torch.bfloat16)
+    for invalid in (1, 0, "fused", None):
+        with pytest.raises(TypeError, match="fused_rope must be a bool"):
+            remnant.unpack_gather_bf16(pool, index, index, lengths, freqs, output,
+                                       fused_rope=invalid)
+    with pytest.raises(ValueError, match="equal shape"):
+        remnant.unpack_gather_bf16(pool, index, index[:, :0], lengths, freqs, output)
+    with pytest.raises(ValueError, match="complex"):
+        remnant.unpack_gather_bf16(pool, index, index, lengths, torch.ones(16, 64), output)
+    with pytest.raises(ValueError, match="int32"):
+        remnant.unpack_gather_bf16(pool, index.long(), index.long(), lengths, freqs, output)
+    # empty selections return the untouched output and launch nothing
+    for physical, raw, active in ((index[:0], index[:0], lengths[:0]),
+                                  (index[:, :0], index[:, :0], lengths)):
+        got = remnant.unpack_gather_bf16(pool, physical, raw, active, freqs, output,
+                                         fused_rope=True)
+        assert got is output and torch.all(output == -91)
+    with pytest.raises(ValueError, match="GPU"):
+        remnant.unpack_gather_bf16(pool, index, index, lengths, freqs, output)
+
+
+def test_pack_and_decode_host_validation():
+    pool = remnant.LatentPool(1, device="cpu")
+    x = torch.zeros((2, 512))
+    loc = torch.zeros(2, dtype=torch.int32)
+    w = torch.ones(512)
+    with pytest.raises(ValueError, match="loc"):
+        remnant.pack_rows_fused(x, w, 1e-6, loc.long(), pool)
+    with pytest.raises(ValueError, match="float32 or bfloat16"):
+        remnant.pack_rows_fused(x.half(), w, 1e-6, loc, pool)
+    remnant.pack_rows_fused(x[:0], w, 1e-6, loc[:0], pool)  # empty: nothing happens
+    native = remnant.LatentPool(1, fmt="native", device="cpu")
+    with pytest.raises(ValueError, match="Packed"):
+        remnant.pack_rows_fused(x, w, 1e-6, loc, native)
+    q = torch.zeros((1, 1, 16, 512), dtype=torch.bfloat16)
+    bt = torch.zeros((1, 1), dtype=torch.int32)
+    idx = torch.zeros((1, 1, 4), dtype=torch.int32)
+    with pytest.raises(ValueError, match="format"):
+        remnant.remnant_sparse_decode_fwd(q, native, bt, idx)
+    with pytest.raises(ValueError, match="multiple of 16"):
+        remnant.remnant_sparse_decode_fwd(q[:, :, :8], pool, bt, idx)
+    with pytest.raises(ValueError, match="freqs_cis"):
+        remnant.flash_mla._decode(False, q, native, bt, idx, seqlens=None, topk_length=None,
+                                  sink=None, freqs_cis=torch.ones(4, 32, dtype=torch.complex64),
+                                  softmax_scale=None, out=None, lse=None, workspace=None,
+                                  layer_id=None)
+
+
+def test_cache_format_configuration():
+    try:
+        assert remnant.configure_cache_format("direct").packed
+        assert remnant.packed_profile()["record_bytes"] == 328
+        assert not remnant.configure_cache_format("native").packed
+        assert remnant.packed_profile()["record_bytes"] == 584
+        for bad in (dict(fmt="fp4"), dict(fmt="remnant", keep_count=192),
+                    dict(fmt="remnant", decode_impl="triton"),
+                    dict(fmt="remnant", layer_keep_counts=[256, 128])):
+            with pytest.raises(ValueError):
+                remnant.configure_cache_format(**bad)
+        import argparse
+        p = argparse.ArgumentParser()
+        config.add_cli_arguments(p)
+        assert config.configure_from_args(p.parse_args(["--kv-cache-format", "direct"])).packed
+        with pytest.raises(SystemExit):
+            p.parse_args(["--kv-cache-format", "remnant256"])
+    finally:
+        remnant.configure_cache_format("native")
+
+
+def test_pool_planes_and_capacity():
+    pool = remnant.LatentPool(3, device="cpu")
+    assert pool.nbytes() == 3 * 20992 and pool.rows == 192
+    assert pool.values().shape == (3, 64, 256)
+    assert pool.bitmaps().shape == (3, 64, 64)
+    assert pool.scales().shape == (3, 64, 8)
+    pool.values()[1, 5] = 7
+    pool.bitmaps()[1, 5] = 9
+    pool.scales()[1, 5] = 11
+    rec = pool.records(torch.tensor([69]))
+    assert rec.shape == (1, 328)
+    assert torch.all(rec[0, :256] == 7) and torch.all(rec[0, 256:320] == 9)
+    assert torch.all(rec[0, 320:] == 11)
+    # the data row of slot 69 starts 16-byte aligned inside its page
+    assert (5 * 320) % 16 == 0 and config.PACKED_PAGE_BYTES % 16 == 0
+    hbm = 288 * 10**9
+    packed, native = remnant.records_fitting(hbm, "direct"), remnant.records_fitting(hbm, "native")
+    assert abs(packed / 878.0e6 - 1) < 1e-3 and abs(native / 493.2e6 - 1) < 1e-3
+    assert abs(packed / native - 584 / 328) < 1e-3

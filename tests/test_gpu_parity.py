@@ -1,0 +1,260 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars: pack bytes bit-exact; reconstruct bit-exact (pre-RoPE and with RoPE);
+top-k gather exact; decode output within BF16 max-abs <= 2e-2 and cosine
+>= 0.9999 of the oracle's float64 attention, LSE within 2e-2.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import remnant
+from remnant import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+W1 = np.ones(512, np.float32)
+OUT_TOL = 2e-2
+COS_MIN = 0.9999
+
+
+def banner(msg):
+    print(f"[gpu-parity] {msg}", flush=True)
+
+
+def gpu_pack(x: torch.Tensor, slots: np.ndarray, pages: int, weight=None, eps=1e-6, fill=0):
+    pool = remnant.LatentPool(pages, fmt="remnant", device=DEV)
+    pool.buffer.fill_(fill)
+    w = torch.ones(512) if weight is None else torch.as_tensor(weight)
+    remnant.pack_rows_fused(x.to(DEV), w.float().to(DEV), eps,
+                            torch.as_tensor(slots, dtype=torch.int32).to(DEV), pool)
+    torch.cuda.synchronize()
+    return pool
+
+
+def oracle_pack(x: torch.Tensor, slots, pages, weight=None, eps=1e-6, fill=0):
+    pool = np.full((pages, oracle.PAGE_BYTES), fill, np.uint8)
+    w = W1 if weight is None else np.asarray(weight, np.float32)
+    oracle.pack_rows_paged(x.float().numpy(), w, eps, np.asarray(slots, np.int32), pool)
+    return pool
+
+
+def assert_pool_equal(gpu_pool, ref_pool):
+    got = gpu_pool.layer().cpu().numpy()
+    diff = np.nonzero(got != ref_pool)
+    assert diff[0].size == 0, f"{diff[0].size} bytes differ, first at page {diff[0][:4]} byte {diff[1][:4]}"
+
+
+# ---- pack -------------------------------------------------------------------------
+
+def test_pack_bit_exact_4096_records_shuffled_slots():
+    banner("pack 4096 bf16 records")
+    x = syn.latents(4096)
+    slots = np.random.default_rng(1).permutation(4096).astype(np.int32)
+    assert_pool_equal(gpu_pack(x, slots, 64), oracle_pack(x, slots, 64))
+
+
+def test_pack_bit_exact_fp32_input_and_weight():
+    banner("pack fp32 input, non-unit weight")
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(1024, 512, generator=g) * torch.linspace(0.1, 10, 512)
+    w = np.linspace(0.5, 1.5, 512).astype(np.float32)
+    slots = np.arange(1024, dtype=np.int32)
+    assert_pool_equal(gpu_pack(x, slots, 16, weight=w, eps=1e-5),
+                      oracle_pack(x, slots, 16, weight=w, eps=1e-5))
+
+
+def test_pack_bit_exact_tie_rows():
+    """Reference tie rows (arange, -arange, zeros), heavy integer ties, signed
+    zeros, constant rows and the 256-survivor closed-form row."""
+    banner("pack tie rows")
+    rng = np.random.default_rng(4)
+    rows = [np.arange(512), -np.arange(512), np.zeros(512), np.ones(512),
+            (np.arange(512) % 2).astype(np.float64)]
+    ints = rng.integers(-6, 7, (59, 512)).astype(np.float32)
+    ints[ints == 0] = -0.0
+    x = torch.from_numpy(np.concatenate([np.stack(rows).astype(np.float32), ints]))
+    for dtype in (torch.float32, torch.bfloat16):
+        slots = np.arange(64, dtype=np.int32)
+        assert_pool_equal(gpu_pack(x.to(dtype), slots, 1),
+                          oracle_pack(x.to(dtype), slots, 1))
+
+
+def test_pack_skips_out_of_range_slots_and_leaves_canaries():
+    banner("pack invalid slots")
+    x = syn.latents(128, seed=5)
+    slots = np.arange(128, dtype=np.int32)
+    slots[::7] = -1
+    slots[5] = 64 * 3  # one past the pool
+    ref = oracle_pack(x, slots, 3, fill=0x5A)
+    assert_pool_equal(gpu_pack(x, slots, 3, fill=0x5A), ref)
+
+
+# ---- reconstruct ----------------------------------------------------------------------
+
+def test_unpack_gather_bit_exact_with_rope_invalid_and_strided():
+    banner("unpack_gather with RoPE")
+    pages = 8
+    x = syn.latents(pages * 64, seed=6)
+    slots = np.random.default_rng(6).permutation(pages * 64).astype(np.int32)
+    pool = gpu_pack(x, slots, pages)
+    ref_pool = pool.layer().cpu().numpy()
+    rng = np.random.default_rng(7)
+    nq, nk = 5, 96
+    physical = rng.integers(-2, pages * 64 + 3, (nq, 2 * nk)).astype(np.int32)[:, ::2]
+    raw = rng.integers(-1, 130, (nq, 2 * nk)).astype(np.int32)[:, ::2]
+    lengths = np.array([96, 0, 50, 95, 1], np.int32)
+    freqs = syn.rope_freqs(4 * 128)  # raw >= 128 is beyond the table
+    ph = torch.from_numpy(rng.integers(0, 1, (nq, 2 * nk)).astype(np.int32))
+    ph[:, ::2] = torch.from_numpy(physical)
+    rw = torch.from_numpy(rng.integers(0, 1, (nq, 2 * nk)).astype(np.int32))
+    rw[:, ::2] = torch.from_numpy(raw)
+    ph_d, rw_d = ph.to(DEV)[:, ::2], rw.to(DEV)[:, ::2]  # strided views
+    out = torch.full((nq * nk + 3, 512), -91.0, dtype=torch.bfloat16, device=DEV)
+    remnant.unpack_gather_bf16(pool, ph_d, rw_d, torch.from_numpy(lengths).to(DEV),
+                               freqs.to(DEV), out, fused_rope=True)
+    torch.cuda.synchronize()
+    expect = oracle.unpack_gather(ref_pool, physical, raw, lengths,
+                                  torch.view_as_real(freqs).numpy())
+    got = syn.bf16_bits(out)
+    assert np.array_equal(got[:nq * nk], expect)
+    assert np.all(out[nq * nk:].float().cpu().numpy() == -91)
+    # the split/pre-RoPE reader equals the dense dequantisation
+    out2 = torch.empty((nq * nk, 512), dtype=torch.bfloat16, device=DEV)
+    remnant.unpack_gather_bf16(pool, ph_d, None, torch.from_numpy(lengths).to(DEV), None, out2)
+    torch.cuda.synchronize()
+    expect2 = oracle.unpack_gather(ref_pool, physical, None, lengths)
+    assert np.array_equal(syn.bf16_bits(out2), expect2)
+
+
+def test_reconstruct_roundtrip_all_records():
+    """pack -> unpack_rows equals the oracle's dense simulation of every record."""
+    banner("reconstruct round trip")
+    x = syn.latents(2048, seed=8)
+    slots = np.random.default_rng(8).permutation(2048).astype(np.int32)
+    pool = gpu_pack(x, slots, 32)
+    rows = remnant.unpack_rows(pool, torch.from_numpy(slots).to(DEV))
+    torch.cuda.synchronize()
+    _, _, _, keep = oracle.pack_rows(x.float().numpy()[:256], W1, 1e-6)
+    sim = oracle.simulate_rows(x.float().numpy()[:256], keep, W1, 1e-6)
+    assert np.array_equal(syn.bf16_bits(rows)[:256], sim)
+
+
+def test_native_store_bit_exact():
+    banner("native store")
+    x = syn.latents(640, seed=9)
+    slots = np.random.default_rng(9).permutation(640).astype(np.int32)
+    positions = np.arange(640, dtype=np.int32)
+    freqs = syn.rope_freqs(4 * 640)
+    pool = remnant.LatentPool(10, fmt="native", device=DEV)
+    remnant.native_store_rows(x.to(DEV), torch.ones(512, device=DEV), 1e-6,
+                              torch.from_numpy(slots).to(DEV), torch.from_numpy(positions).to(DEV),
+                              freqs.to(DEV), pool)
+    torch.cuda.synchronize()
+    ref = np.zeros((10, oracle.NATIVE_PAGE_BYTES), np.uint8)
+    oracle.native_pack_rows_paged(x.float().numpy(), W1, 1e-6, slots, positions,
+                                  torch.view_as_real(freqs).numpy(), ref)
+    assert np.array_equal(pool.layer().cpu().numpy(), ref)
+
+
+# ---- decode -----------------------------------------------------------------------------
+
+def build_decode_case(contexts, q_len, heads, topk, seed, packed=True, sink=True):
+    x = syn.latents(sum(contexts), seed=seed)
+    table, pages = syn.paged_requests(contexts, seed)
+    n_pages = max(pages, 1)
+    # logical record r of request b -> slot table[b, r // 64] * 64 + r % 64
+    slots, positions = [], []
+    for b, c in enumerate(contexts):
+        r = np.arange(c)
+        slots.append(table[b, r // 64] * 64 + r % 64)
+        positions.append(r)
+    slots = np.concatenate(slots).astype(np.int32)
+    positions = np.concatenate(positions).astype(np.int32)
+    freqs = syn.rope_freqs(4 * max(contexts))
+    pool = remnant.LatentPool(n_pages, fmt="remnant" if packed else "native", device=DEV)
+    if packed:
+        remnant.pack_rows_fused(x.to(DEV), torch.ones(512, device=DEV), 1e-6,
+                                torch.from_numpy(slots).to(DEV), pool)
+    else:
+        remnant.native_store_rows(x.to(DEV), torch.ones(512, device=DEV), 1e-6,
+                                  torch.from_numpy(slots).to(DEV),
+                                  torch.from_numpy(positions).to(DEV), freqs.to(DEV), pool)
+    idx, lens = syn.topk_indices(contexts, q_len, topk, seed + 1)
+    g = torch.Generator().manual_seed(seed + 2)
+    q = (torch.randn(len(contexts), q_len, heads, 512, generator=g) * 0.5).to(torch.bfloat16)
+    sink_t = torch.randn(heads, generator=g) if sink else None
+    return dict(pool=pool, table=table, idx=idx, lens=lens, q=q, sink=sink_t, freqs=freqs,
+                contexts=contexts, packed=packed)
+
+
+def run_decode(c):
+    q = c["q"].to(DEV)
+    kw = dict(seqlens=torch.tensor(c["contexts"], dtype=torch.int32, device=DEV),
+              topk_length=torch.from_numpy(c["lens"]).to(DEV),
+              sink=None if c["sink"] is None else c["sink"].to(DEV))
+    bt = torch.from_numpy(c["table"]).to(DEV)
+    idx = torch.from_numpy(c["idx"]).to(DEV)
+    if c["packed"]:
+        out, lse = remnant.remnant_sparse_decode_fwd(q, c["pool"], bt, idx,
+                                                     freqs_cis=c["freqs"].to(DEV), **kw)
+    else:
+        out, lse = remnant.native_sparse_decode_fwd(q, c["pool"], bt, idx, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), lse.cpu().numpy()
+
+
+def oracle_decode(c):
+    pool = c["pool"].layer().cpu().numpy()
+    return oracle.sparse_decode(
+        syn.bf16_bits(c["q"]).reshape(c["q"].shape), pool, c["packed"], c["table"],
+        np.array(c["contexts"], np.int32), c["idx"], c["lens"],
+        None if c["sink"] is None else c["sink"].numpy(),
+        torch.view_as_real(c["freqs"]).numpy() if c["packed"] else None, 1 / np.sqrt(512))
+
+
+def check_decode(c):
+    out, lse = run_decode(c)
+    ref, ref_lse = oracle_decode(c)
+    err = np.abs(out - ref).max()
+    cos = syn.cosine(out, ref)
+    assert err <= OUT_TOL, f"max-abs {err}"
+    assert cos >= COS_MIN, f"cosine {cos}"
+    finite = np.isfinite(ref_lse)
+    assert np.array_equal(finite, np.isfinite(lse))
+    assert np.abs(lse[finite] - ref_lse[finite]).max() <= OUT_TOL
+    return err, cos
+
+
+@pytest.mark.parametrize("packed", [True, False], ids=["direct", "native"])
+def test_decode_small_batch_with_padding_and_sink(packed):
+    banner(f"decode small packed={packed}")
+    c = build_decode_case([300, 70, 1000], q_len=1, heads=16, topk=256, seed=11, packed=packed)
+    c["idx"][1, 0, 3] = 5000  # beyond the request's records -> ignored
+    c["idx"][2, 0, 7] = c["idx"][2, 0, 8]  # duplicate counts twice
+    check_decode(c)
+
+
+def test_decode_batch1_topk2048_context_8192():
+    """One GPU's 16-head share, 32k-token context (8192 records), top-k 2048."""
+    banner("decode B=1 H=16 topk=2048")
+    c = build_decode_case([8192], q_len=1, heads=16, topk=2048, seed=12, sink=False)
+    check_decode(c)
+
+
+def test_decode_next_n2_and_32_heads():
+    banner("decode Sq=2 H=32")
+    c = build_decode_case([700, 2000], q_len=2, heads=32, topk=512, seed=13)
+    check_decode(c)
+
+
+def test_decode_empty_selection_gives_zero_and_sink_lse():
+    banner("decode empty selection")
+    c = build_decode_case([64], q_len=1, heads=16, topk=64, seed=14)
+    c["lens"][:] = 0
+    out, lse = run_decode(c)
+    assert np.all(out == 0)
+    np.testing.assert_allclose(lse.ravel(), c["sink"].numpy(), rtol=1e-6, atol=1e-6)
