@@ -1,0 +1,330 @@
+"""Benchmark of the MI355X packed-KV hot path (one GPU).
+
+Headline workload (one "step"): pack 1,048,576 synthetic C4 records (BF16
+512-coordinate latents) into a paged pool of 64 records per page through a
+seeded random slot permutation, then reconstruct all of them to dense BF16
+rows (gather through the same permutation, pre-RoPE). ``value`` is records/s
+through pack + reconstruct with inputs resident in HBM.
+
+Also reported on the same JSON line:
+  roofline      dominant kernel's algorithmic bytes / HIP-event-timed duration
+                against MI355X's 8 TB/s HBM peak (traffic from the committed
+                rocprofv3 counter runs when available);
+  kernels       per-kernel timings (pack, reconstruct, reconstruct+RoPE);
+  decode        Direct packed vs Native sparse decode: batch 1 (16 heads, top-k
+                2048, 8192-record context), batch 64 (log-uniform 4k-128k token
+                contexts), batch 128 x next-n 2 at 128k-token contexts on a
+                pool sized to most of HBM (capacity case);
+  cpu_baseline  the CPU oracle (single thread) on a bounded sample of the
+                same workload, timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "flash-optimizations_amd")]
+
+METRIC = "packed sparse-MLA decode µs/step + HBM GB/s; pack/reconstruct records/s"
+HBM_PEAK_GBS = 8000.0
+PACK_BYTES = 1024 + 328 + 4          # bf16 row in, record out, slot index
+RECON_BYTES = 328 + 4 + 1024         # record in, physical index, bf16 row out
+RECON_ROPE_BYTES = RECON_BYTES + 4 + 256  # + raw index + complex64 frequency row
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--records", type=int, default=1 << 20)
+    p.add_argument("--quick", action="store_true", help="skip decode, capacity and CPU legs")
+    p.add_argument("--no-capacity", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-sample", type=int, default=196608)
+    return p.parse_args()
+
+
+def events(torch, n):
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def bulk(torch, remnant, args):
+    """Pack + reconstruct of args.records records; returns timings (ms)."""
+    dev = "cuda"
+    n = args.records
+    g = torch.Generator(device=dev).manual_seed(20260919)
+    gc = torch.Generator().manual_seed(20260919)
+    sigma = torch.exp(torch.empty(512).uniform_(math.log(0.1), math.log(10.0), generator=gc))
+    x = (torch.randn(n, 512, device=dev, generator=g) * sigma.to(dev)).to(torch.bfloat16)
+    slots = torch.randperm(n, device=dev, generator=g).to(torch.int32)
+    pool = remnant.LatentPool((n + 63) // 64, device=dev)
+    w = torch.ones(512, device=dev)
+    out = torch.empty((n, 512), dtype=torch.bfloat16, device=dev)
+    physical = slots.view(1, n)
+    raw = torch.arange(n, dtype=torch.int32, device=dev).view(1, n)
+    lengths = torch.full((1,), n, dtype=torch.int32, device=dev)
+    freqs = remnant.synthetic.rope_freqs(4 * n).to(dev)
+
+    def pack():
+        remnant.pack_rows_fused(x, w, 1e-6, slots, pool)
+
+    def recon():
+        remnant.unpack_gather_bf16(pool, physical, None, lengths, None, out)
+
+    def recon_rope():
+        remnant.unpack_gather_bf16(pool, physical, raw, lengths, freqs, out, fused_rope=True)
+
+    for _ in range(args.warmup):
+        pack()
+        recon()
+    torch.cuda.synchronize()
+    k = args.steps
+    ev = events(torch, 3 * k)
+    t0 = time.perf_counter()
+    for i in range(k):
+        ev[3 * i].record()
+        pack()
+        ev[3 * i + 1].record()
+        recon()
+        ev[3 * i + 2].record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    pack_ms = [ev[3 * i].elapsed_time(ev[3 * i + 1]) for i in range(k)]
+    recon_ms = [ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(k)]
+    total_ms = ev[0].elapsed_time(ev[3 * k - 1])
+    # reconstruct with the RoPE frequency table, separately
+    for _ in range(2):
+        recon_rope()
+    e2 = events(torch, 2)
+    e2[0].record()
+    for _ in range(k):
+        recon_rope()
+    e2[1].record()
+    torch.cuda.synchronize()
+    rope_ms = e2[0].elapsed_time(e2[1]) / k
+    return dict(n=n, steps=k, total_ms=total_ms, wall_ms=wall, pack_ms=pack_ms,
+                recon_ms=recon_ms, rope_ms=rope_ms)
+
+
+def build_decode(torch, remnant, contexts, q_len, topk, packed, seed, pool_pages=None):
+    """Pack the contexts' records into a (possibly much larger) paged pool."""
+    syn = remnant.synthetic
+    dev = "cuda"
+    table, pages = syn.paged_requests(contexts, seed, pool_pages)
+    pool = remnant.LatentPool(pages, fmt="remnant" if packed else "native", device=dev)
+    freqs = syn.rope_freqs(4 * max(contexts)).to(dev)
+    w = torch.ones(512, device=dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    gc = torch.Generator().manual_seed(seed)
+    sigma = torch.exp(torch.empty(512).uniform_(math.log(0.1), math.log(10.0), generator=gc)).to(dev)
+    tab = torch.from_numpy(table).to(dev)
+    for b, c in enumerate(contexts):
+        for lo in range(0, c, 1 << 16):
+            hi = min(c, lo + (1 << 16))
+            r = torch.arange(lo, hi, device=dev, dtype=torch.int64)
+            slot = (tab[b, r // 64].to(torch.int64) * 64 + r % 64).to(torch.int32)
+            x = (torch.randn(hi - lo, 512, device=dev, generator=g) * sigma).to(torch.bfloat16)
+            if packed:
+                remnant.pack_rows_fused(x, w, 1e-6, slot, pool)
+            else:
+                remnant.native_store_rows(x, w, 1e-6, slot, r.to(torch.int32), freqs, pool)
+    idx, lens = syn.topk_indices(contexts, q_len, topk, seed + 1)
+    q = (torch.randn(len(contexts), q_len, 16, 512, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    sink = torch.randn(16, device=dev, generator=g)
+    return dict(pool=pool, table=tab, idx=torch.from_numpy(idx).to(dev),
+                lens=torch.from_numpy(lens).to(dev),
+                seqlens=torch.tensor(contexts, dtype=torch.int32, device=dev), q=q, sink=sink,
+                freqs=freqs, packed=packed, valid=int(lens.sum()))
+
+
+def time_decode(torch, remnant, c, reps=10, warm=5, samples=20):
+    """Median µs per decode call, from HIP-graph replays of `reps` calls."""
+    tokens, heads = c["q"].shape[0] * c["q"].shape[1], c["q"].shape[2]
+    _, need = remnant.get_decode_metadata(tokens, heads, c["idx"].shape[-1])
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(c["q"])
+    lse = torch.empty(c["q"].shape[:3], dtype=torch.float32, device="cuda")
+    kw = dict(seqlens=c["seqlens"], topk_length=c["lens"], sink=c["sink"], out=out, lse=lse,
+              workspace=ws)
+
+    def call():
+        if c["packed"]:
+            remnant.remnant_sparse_decode_fwd(c["q"], c["pool"], c["table"], c["idx"],
+                                              freqs_cis=c["freqs"], **kw)
+        else:
+            remnant.native_sparse_decode_fwd(c["q"], c["pool"], c["table"], c["idx"], **kw)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            call()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            call()
+    for _ in range(warm):
+        graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(samples):
+        e = events(torch, 2)
+        e[0].record()
+        graph.replay()
+        e[1].record()
+        e[1].synchronize()
+        times.append(e[0].elapsed_time(e[1]) * 1e3 / reps)
+    return statistics.median(times), out, lse
+
+
+def decode_bytes(c, rope_table: bool):
+    rec = 328 if c["packed"] else 584
+    per = rec + (256 if (rope_table and c["packed"]) else 0)
+    tokens, heads = c["q"].shape[0] * c["q"].shape[1], c["q"].shape[2]
+    return c["valid"] * per + 2 * tokens * heads * 512 * 2 + c["idx"].numel() * 4
+
+
+def decode_leg(torch, remnant, args):
+    syn = remnant.synthetic
+    res = {}
+    cases = [("b1_h16_topk2048_ctx8192", [8192], 1, {}),
+             ("b64_h16_topk2048_ctx4k_128k", syn.log_uniform_contexts(64, 4096, 131072, 7), 1, {})]
+    if not args.no_capacity:
+        free, total = torch.cuda.mem_get_info()
+        res["hbm_total_bytes"] = total
+        cap_pages = int(0.6 * free) // remnant.config.NATIVE_PAGE_BYTES
+        cases.append(("b128_sq2_h16_topk2048_ctx128k", [32768] * 128, 2,
+                      {"pool_pages": cap_pages}))
+    for name, contexts, q_len, extra in cases:
+        entry = {"batch": len(contexts), "q_len": q_len, "heads": 16, "topk": 2048,
+                 "context_records_mean": float(sum(contexts) / len(contexts))}
+        for packed in (True, False):
+            log(f"decode {name} packed={packed}")
+            c = build_decode(torch, remnant, contexts, q_len, 2048, packed, 11,
+                             extra.get("pool_pages"))
+            us, _, _ = time_decode(torch, remnant, c)
+            key = "direct_packed" if packed else "native"
+            byt = decode_bytes(c, rope_table=False)
+            entry[key] = {"us_per_step": us, "tokens_per_s": c["q"].shape[0] * q_len / (us * 1e-6),
+                          "algorithmic_bytes": byt, "GBps": byt / (us * 1e3),
+                          "hbm_frac": byt / (us * 1e3) / HBM_PEAK_GBS,
+                          "pool_bytes": c["pool"].nbytes()}
+            if packed:
+                entry[key]["algorithmic_bytes_with_rope_table"] = decode_bytes(c, True)
+            del c
+            torch.cuda.empty_cache()
+        entry["packed_over_native_time"] = entry["direct_packed"]["us_per_step"] / entry["native"]["us_per_step"]
+        res[name] = entry
+    return res
+
+
+def cpu_leg(args):
+    """Oracle (plain C, one thread) on a bounded sample of the bulk workload."""
+    import numpy as np
+
+    import oracle
+    n = args.cpu_sample
+    x = oracle.synthetic_latents(n)
+    slots = np.random.default_rng(1).permutation(n).astype(np.int32)
+    pool = np.zeros(((n + 63) // 64, oracle.PAGE_BYTES), np.uint8)
+    t0 = time.perf_counter()
+    oracle.pack_rows_paged(x, np.ones(512, np.float32), 1e-6, slots, pool)
+    t1 = time.perf_counter()
+    oracle.unpack_gather(pool, slots[None], None, np.array([n], np.int32))
+    t2 = time.perf_counter()
+    return {"value": n / (t2 - t0), "unit": "records/s", "cores": 1, "kind": "port",
+            "sample": f"{n} of the 1,048,576-record pack + reconstruct workload, one thread "
+                      f"(pack {n / (t1 - t0):.0f} rec/s, reconstruct {n / (t2 - t1):.0f} rec/s)",
+            "host_cpus": os.cpu_count()}
+
+
+def load_traffic():
+    """HBM bytes per launch from the committed rocprofv3 counter summaries."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            return json.load(f)
+    return {}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus above 1 is not "
+                                   "supported (no inter-GPU path is built)"}))
+        sys.exit(2)
+    import torch
+
+    import remnant
+    import remnant.synthetic  # noqa: F401
+    torch.cuda.set_device(0)
+    log(f"bulk pack + reconstruct, {args.records} records")
+    b = bulk(torch, remnant, args)
+    n = b["n"]
+    ms_per_step = b["total_ms"] / b["steps"]
+    pack_ms = statistics.mean(b["pack_ms"])
+    recon_ms = statistics.mean(b["recon_ms"])
+    kernels = {
+        "pack": {"ms": pack_ms, "records_per_s": n / (pack_ms * 1e-3),
+                 "GBps": n * PACK_BYTES / (pack_ms * 1e6)},
+        "reconstruct": {"ms": recon_ms, "records_per_s": n / (recon_ms * 1e-3),
+                        "GBps": n * RECON_BYTES / (recon_ms * 1e6)},
+        "reconstruct_rope_table": {"ms": b["rope_ms"], "records_per_s": n / (b["rope_ms"] * 1e-3),
+                                   "GBps": n * RECON_ROPE_BYTES / (b["rope_ms"] * 1e6)},
+    }
+    dominant = "pack" if pack_ms >= recon_ms else "reconstruct"
+    dom_ms = pack_ms if dominant == "pack" else recon_ms
+    dom_bytes = n * (PACK_BYTES if dominant == "pack" else RECON_BYTES)
+    achieved = dom_bytes / (dom_ms * 1e6)
+    traffic = load_traffic().get(dominant)
+    line = {
+        "metric": METRIC,
+        "value": n / (ms_per_step * 1e-3),
+        "unit": "records/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "bulk pack + reconstruct of 1,048,576 C4 records (BF16 "
+                               "512-coordinate latents, N(0,1) x log-uniform[0.1,10] per-coordinate "
+                               "sigma, seed 20260919) into 64-record pages through a seeded random "
+                               "slot permutation; reconstruct pre-RoPE",
+                   "records": n, "record_bytes": 328, "page_records": 64},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel": dominant,
+                     "algorithmic_bytes_per_launch": dom_bytes,
+                     "avg_launch_ms": dom_ms},
+        "kernels": kernels,
+    }
+    if not args.quick:
+        line["decode"] = decode_leg(torch, remnant, args)
+    if not (args.quick or args.no_cpu):
+        log("cpu baseline (oracle, one thread)")
+        line["cpu_baseline"] = cpu_leg(args)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

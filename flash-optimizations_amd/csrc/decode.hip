@@ -8,17 +8,25 @@
 //   l_j = (q_h . K_j) * scale, Z = sum_j exp(l_j) + exp(sink_h),
 //   out = sum_j exp(l_j) K_j / Z, lse = ln Z.
 //
-// Work split: one wave64 per (split, token, 16-head block). A split walks its
-// share of the top-k list in tiles of 16 records:
-//   1. gather: record r -> page block_table[b, r/64], row r%64;
-//   2. dequantize the tile (with tail RoPE for Packed) into an LDS tile
-//      K[16][512] BF16 -- lanes 4r..4r+3 each expand 128 coordinates of record r;
-//   3. S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (Q held in registers);
-//   4. online softmax in the log2 domain (one head per lane column);
-//   5. O += P K on v_mfma_f32_16x16x16_bf16 (P taken straight from the S^T
-//      accumulator layout, K read from the LDS tile).
-// Splits write (O/l, log2 l + m) partials that a combine kernel merges with
-// the sink; a single split finalises in place.
+// Work split. A workgroup of 4 waves owns (split, token, 16-head block) and
+// walks its share of the top-k list in tiles of 32 records:
+//   * record metadata (index -> block table -> page/row, validity) for the
+//     whole share is resolved once into LDS;
+//   * the next tile's record bytes (and its RoPE rows) are loaded into
+//     registers while the current tile computes, then written to LDS staging;
+//   * dequantization: thread (record r, bitmap word w) expands coordinates
+//     64w..64w+63 -- v_perm places the kept E4M3 codes (zeros for pruned lanes)
+//     using a 256-entry selector table, v_cvt_scalef32_pk_bf16_fp8 applies the
+//     UE8M0 scale, the tail word is BF16-rounded then rotated -- into a dense
+//     BF16 tile K[32][512] in LDS;
+//   * QK: wave w contracts its 128-coordinate quarter (S^T = K Q^T on
+//     v_mfma_f32_16x16x32_bf16); the 4 partial S^T tiles are summed through LDS;
+//   * online softmax in the log2 domain (identical in every wave);
+//   * PV: wave w accumulates O[16 heads][its 128 coordinates] on
+//     v_mfma_f32_16x16x32_bf16, the P operand taken straight from the S^T
+//     accumulator layout and the K operand read with ds_read_b64_tr_b16.
+// A split count > 1 writes (O/l, m + log2 l) partials merged with the sink by a
+// combine kernel; a single split finalises in place.
 #include "remnant_device.h"
 #include "remnant_mi355x.h"
 
@@ -26,12 +34,18 @@ using namespace rm;
 
 namespace {
 
-constexpr int kTile = 16;
-constexpr int kKdStride = kHeadDim + 8;  // BF16 elements per LDS row (pad vs bank conflicts)
+constexpr int kT = 32;                     // records per tile
+constexpr int kThreads = 256;              // 4 waves
+constexpr int kKdStride = kHeadDim + 8;    // BF16 per LDS row (1040 B, 16-B aligned)
+constexpr int kMaxChunk = 1024;            // records per split
+constexpr int kMaxSplits = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -50,7 +64,7 @@ struct DecodeArgs {
   float scale_log2;
   int64_t q_len;
   int64_t heads;
-  int chunk;       // records per split (multiple of kTile)
+  int chunk;       // records per split (multiple of kT, <= kMaxChunk)
   int splits;
   uint16_t* out;
   float* lse;
@@ -58,106 +72,50 @@ struct DecodeArgs {
   float* ws_lse;   // [tokens, splits, heads]
 };
 
-// Expand 8 coordinates of a Packed record (bitmap byte MSB-first, kept codes
-// as the next bytes of `run`) to BF16-rounded floats.
-__device__ __forceinline__ void expand8(uint32_t bits, uint64_t run, float scale, float* v) {
-  int used = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const bool kept = (bits >> (7 - i)) & 1u;
-    const uint32_t code = (uint32_t)(run >> (8 * used)) & 0xffu;
-    v[i] = kept ? e4m3_to_f32(code) * scale : 0.0f;
-    used += kept ? 1 : 0;
-  }
-}
+template <bool kPacked>
+struct Geo {
+  static constexpr int kData = kPacked ? kDataBytes : kNativeDataBytes;
+  static constexpr int kPage = kPacked ? kPageBytes : kNativePageBytes;
+  static constexpr int kStage = kData + 16;             // data row + 8 scale bytes + pad
+  static constexpr int kDataChunks = kT * kData / 16;   // 16-byte pieces per tile
+  static constexpr int kDataLoads = (kDataChunks + kThreads - 1) / kThreads;
+  static constexpr int kFreqLoads = kPacked ? (kT * 256 / 16) / kThreads : 0;  // 2
+};
+
+template <bool kPacked>
+struct Smem {
+  uint16_t kd[kT * kKdStride];                       // dense BF16 tile
+  uint8_t stage[kT * Geo<kPacked>::kStage];          // raw records of the tile
+  float freq[kPacked ? kT * 64 : 1];                 // RoPE rows of the tile
+  f32x4 spart[4][2][64];                             // per-wave partial S^T
+  uint64_t sel[kPacked ? 256 : 1];                   // v_perm selectors per bitmap byte
+  int32_t rec[kMaxChunk];                            // slot (page*64+row) or -1
+  int32_t raw[kMaxChunk];
+};
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return bf16_rne(a) | (bf16_rne(b) << 16);
 }
 
-// Lane (record rec, quarter qt) writes coordinates 128qt..128qt+127 of its record.
-template <bool kPacked>
-__device__ __forceinline__ void dequant_quarter(const DecodeArgs& a, const uint8_t* rec_data,
-                                                const uint8_t* rec_scales, int64_t raw, bool ok,
-                                                int qt, uint16_t* kd_row) {
-  if (!ok) {
-#pragma unroll 4
-    for (int c = 0; c < 16; ++c) *(u32x4*)(kd_row + 128 * qt + 8 * c) = u32x4{0u, 0u, 0u, 0u};
-    return;
-  }
-  if (kPacked) {
-    const u32x4* bm = (const u32x4*)(rec_data + kCodeBytes);
-    const u32x4 b0 = bm[0], b1 = bm[1], b2 = bm[2], b3 = bm[3];
-    const uint64_t w[8] = {((uint64_t)b0[1] << 32) | b0[0], ((uint64_t)b0[3] << 32) | b0[2],
-                           ((uint64_t)b1[1] << 32) | b1[0], ((uint64_t)b1[3] << 32) | b1[2],
-                           ((uint64_t)b2[1] << 32) | b2[0], ((uint64_t)b2[3] << 32) | b2[2],
-                           ((uint64_t)b3[1] << 32) | b3[0], ((uint64_t)b3[3] << 32) | b3[2]};
-    int rank = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rank += i < 2 * qt ? __popcll(w[i]) : 0;
-    const uint64_t wa = qt == 0 ? w[0] : qt == 1 ? w[2] : qt == 2 ? w[4] : w[6];
-    const uint64_t wb = qt == 0 ? w[1] : qt == 1 ? w[3] : qt == 2 ? w[5] : w[7];
-    const float sa = exp2i((int)rec_scales[2 * qt] - 127);
-    const float sb = exp2i((int)rec_scales[2 * qt + 1] - 127);
-    const float* fr = a.freqs ? a.freqs + (raw * 4) * (2 * kRopePairs) : nullptr;
-#pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const uint64_t word = c < 8 ? wa : wb;
-      const uint32_t bits = (uint32_t)(word >> (56 - 8 * (c & 7))) & 0xffu;
-      const int base = rank & ~3;
-      const uint32_t* cw = (const uint32_t*)(rec_data + base);
-      const uint32_t d0 = cw[0], d1 = cw[1], d2 = cw[2];
-      const uint32_t sh = 8u * (uint32_t)(rank & 3);
-      const uint32_t lo = (uint32_t)((((uint64_t)d1 << 32) | d0) >> sh);
-      const uint32_t hi = (uint32_t)((((uint64_t)d2 << 32) | d1) >> sh);
-      float v[8];
-      expand8(bits, ((uint64_t)hi << 32) | lo, c < 8 ? sa : sb, v);
-      rank += __popc(bits);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = bf16_to_f32(bf16_rne(v[i]));
-      const int coord = 128 * qt + 8 * c;
-      if (qt == 3 && c >= 8 && fr) {  // coordinates 448..511: rotate in place
-        // coordinate 448 + 2j is the real part of pair j: (cos, sin) at floats 2j, 2j + 1
-        const float* f = fr + (coord - kNopeDim);
-        const f32x4 x0 = *(const f32x4*)f, x1 = *(const f32x4*)(f + 4);
-        float cs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        rope4(v, cs);
-      }
-      *(u32x4*)(kd_row + coord) = u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                        pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
-    }
-  } else {
-#pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const int coord = 128 * qt + 8 * c;
-      if (coord < kNopeDim) {
-        const u32x2 codes = *(const u32x2*)(rec_data + coord);
-        const float s = exp2i((int)rec_scales[coord / kGroup] - 127);
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[i] = e4m3_to_f32((codes[0] >> (8 * i)) & 0xffu) * s;
-          v[4 + i] = e4m3_to_f32((codes[1] >> (8 * i)) & 0xffu) * s;
-        }
-        *(u32x4*)(kd_row + coord) = u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                          pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
-      } else {
-        *(u32x4*)(kd_row + coord) = *(const u32x4*)(rec_data + kNopeDim + 2 * (coord - kNopeDim));
-      }
-    }
-  }
+// Two E4M3 codes (bytes 0-1, or 2-3 with kHi) times scale -> two BF16 (exact).
+template <bool kHi>
+__device__ __forceinline__ uint32_t cvt2(uint32_t codes, float scale) {
+  bf16x2 r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(codes, scale, kHi);
+  return __builtin_bit_cast(uint32_t, r);
 }
 
 template <bool kPacked>
-__global__ __launch_bounds__(64) void sparse_decode_kernel(DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t kd[kTile * kKdStride];
-  const int lane = wave_lane();
+__global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a) {
+  using G = Geo<kPacked>;
+  __shared__ __attribute__((aligned(16))) Smem<kPacked> sm;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = uniform(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
   const int split = blockIdx.x;
   const int64_t t = blockIdx.y;
-  const int hb = blockIdx.z;
+  const int64_t head0 = (int64_t)blockIdx.z * 16;
   const int64_t b = t / a.q_len;
-  const int g = lane >> 4, col = lane & 15;
-  const int64_t head0 = (int64_t)hb * 16;
 
   int64_t len = a.topk;
   if (a.topk_length) {
@@ -166,72 +124,218 @@ __global__ __launch_bounds__(64) void sparse_decode_kernel(DecodeArgs a) {
   }
   const int64_t k0 = (int64_t)split * a.chunk;
   const int64_t k1 = k0 + a.chunk < len ? k0 + a.chunk : len;
+  const int n = k1 > k0 ? (int)(k1 - k0) : 0;
   const int64_t seqlen = a.seqlens ? a.seqlens[b] : INT64_MAX;
-  const int64_t pool_bytes_page = kPacked ? kPageBytes : kNativePageBytes;
-  const int data_bytes = kPacked ? kDataBytes : kNativeDataBytes;
 
-  // Q^T operand: lane (col = head, g) holds Q[head][32ks + 8g .. +7]
-  bf16x8 qreg[16];
-  {
-    const uint16_t* qh = a.q + ((t * a.heads) + head0 + col) * kHeadDim + 8 * g;
+  // ---- setup: selectors, record metadata, Q operand ----
+  if (kPacked) {
+    // byte bits MSB-first = coordinates 0..7; selector byte i = rank of i or 0x0c (zero)
+    uint32_t s = tid, r = 0;
+    uint64_t sel = 0;
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) qreg[ks] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qh + 32 * ks));
+    for (int i = 0; i < 8; ++i) {
+      const bool kept = (s >> (7 - i)) & 1u;
+      sel |= (uint64_t)(kept ? r : 0x0cu) << (8 * i);
+      r += kept ? 1u : 0u;
+    }
+    sm.sel[tid] = sel;
   }
-  f32x4 o[32];
-#pragma unroll
-  for (int nt = 0; nt < 32; ++nt) o[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.0f;  // softmax state of head `col`
-
-  for (int64_t kt = k0; kt < k1; kt += kTile) {
-    // 1. gather metadata: lanes 0..15 resolve records kt..kt+15
-    const int64_t k = kt + (lane & 15);
-    bool ok = lane < kTile && k < k1;
-    int64_t r = ok ? a.indices[t * a.topk + k] : -1;
-    ok = ok && r >= 0 && r < seqlen && (r >> 6) < a.max_blocks;
+  for (int i = tid; i < n; i += kThreads) {
+    const int64_t r = a.indices[t * a.topk + k0 + i];
+    bool ok = r >= 0 && r < seqlen && (r >> 6) < a.max_blocks;
     int64_t page = ok ? a.block_table[b * a.bt_stride + (r >> 6)] : -1;
     ok = ok && page >= 0 && page < a.pool_pages;
     if (kPacked && a.freqs) ok = ok && r * 4 < a.freq_rows;
-    const uint32_t vmask = (uint32_t)__ballot(ok);
-
-    // 2. dequantize: lane -> record lane/4, quarter lane%4
-    {
-      const int rec = lane >> 2, qt = lane & 3;
-      const int64_t rr = __shfl(r, rec, 64);
-      const int64_t pg = __shfl(page, rec, 64);
-      const bool rok = (vmask >> rec) & 1u;
-      const uint8_t* base = a.pool + (rok ? pg : 0) * pool_bytes_page;
-      const int row = (int)(rr & 63);
-      dequant_quarter<kPacked>(a, base + row * data_bytes,
-                               base + kPageRecords * data_bytes + row * kScaleBytes, rr, rok, qt,
-                               kd + rec * kKdStride);
-    }
-    wave_lds_sync();
-
-    // 3. S^T[rec][head] = K[rec] . Q[head]
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    sm.rec[i] = ok ? (int32_t)(page * 64 + (r & 63)) : -1;
+    sm.raw[i] = (int32_t)r;
+  }
+  bf16x8 qreg[4];  // Q[head col][128 wave + 32 ks + 8 g .. +7]
+  {
+    const uint16_t* qh = a.q + (t * a.heads + head0 + col) * kHeadDim + 128 * wave + 8 * g;
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) {
-      const bf16x8 kv = __builtin_bit_cast(bf16x8, *(const u32x4*)(kd + col * kKdStride + 32 * ks + 8 * g));
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qreg[ks], s, 0, 0, 0);
-    }
-    // lane holds S^T[rec = 4g + i][head = col]
+    for (int ks = 0; ks < 4; ++ks) qreg[ks] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qh + 32 * ks));
+  }
+  f32x4 o[8];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) o[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+  __syncthreads();
 
-    // 4. online softmax (log2 domain)
-    float sv[4];
+  // ---- tile loader: registers <- HBM, LDS staging <- registers ----
+  u32x4 pre[G::kDataLoads];
+  u32x2 pre_scale;
+  u32x4 pre_freq[G::kFreqLoads > 0 ? G::kFreqLoads : 1];
+  auto load_tile = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < G::kDataLoads; ++j) {
+      const int c = tid + j * kThreads;
+      pre[j] = u32x4{0u, 0u, 0u, 0u};
+      if (c < G::kDataChunks) {
+        const int r = c / (G::kData / 16), piece = c % (G::kData / 16);
+        const int slot = base + r < n ? sm.rec[base + r] : -1;
+        if (slot >= 0) {
+          const uint8_t* page = a.pool + (int64_t)(slot >> 6) * G::kPage;
+          pre[j] = *(const u32x4*)(page + (slot & 63) * G::kData + 16 * piece);
+        }
+      }
+    }
+    pre_scale = u32x2{0u, 0u};
+    if (tid < kT) {
+      const int slot = base + tid < n ? sm.rec[base + tid] : -1;
+      if (slot >= 0) {
+        const uint8_t* page = a.pool + (int64_t)(slot >> 6) * G::kPage;
+        pre_scale = *(const u32x2*)(page + kPageRecords * G::kData + (slot & 63) * kScaleBytes);
+      }
+    }
+    if (kPacked) {
+#pragma unroll
+      for (int j = 0; j < G::kFreqLoads; ++j) {
+        const int c = tid + j * kThreads;  // 16 pieces of 16 B per record
+        const int r = c >> 4, piece = c & 15;
+        const int slot = base + r < n ? sm.rec[base + r] : -1;
+        pre_freq[j] = u32x4{0u, 0u, 0u, 0u};
+        if (slot >= 0 && a.freqs) {
+          const int64_t raw = sm.raw[base + r];
+          pre_freq[j] = *(const u32x4*)(a.freqs + raw * 4 * 64 + 4 * piece);
+        }
+      }
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int j = 0; j < G::kDataLoads; ++j) {
+      const int c = tid + j * kThreads;
+      if (c < G::kDataChunks) {
+        const int r = c / (G::kData / 16), piece = c % (G::kData / 16);
+        *(u32x4*)(sm.stage + r * G::kStage + 16 * piece) = pre[j];
+      }
+    }
+    if (tid < kT) *(u32x2*)(sm.stage + tid * G::kStage + G::kData) = pre_scale;
+    if (kPacked) {
+#pragma unroll
+      for (int j = 0; j < G::kFreqLoads; ++j) {
+        const int c = tid + j * kThreads;
+        *(u32x4*)(sm.freq + (c >> 4) * 64 + 4 * (c & 15)) = pre_freq[j];
+      }
+    }
+  };
+
+  if (n > 0) {
+    load_tile(0);
+    store_tile();
+  }
+  __syncthreads();
+
+  for (int base = 0; base < n; base += kT) {
+    // prefetch the next tile while this one computes
+    if (base + kT < n) load_tile(base + kT);
+
+    // ---- dequantize: thread -> record tid/8, bitmap word tid%8 (64 coords) ----
+    {
+      const int r = tid >> 3, w = tid & 7;
+      const uint8_t* st = sm.stage + r * G::kStage;
+      uint16_t* krow = sm.kd + r * kKdStride + 64 * w;
+      if (kPacked) {
+        const uint64_t word = *(const uint64_t*)(st + kCodeBytes + 8 * w);
+        // exclusive prefix of popcounts over the record's 8 words (lanes 8r'..8r'+7)
+        const int pc = __popcll(word);
+        int incl = pc;
+#pragma unroll
+        for (int d = 1; d < 8; d <<= 1) {
+          const int up = __shfl_up(incl, d, 8);
+          incl += (w >= d) ? up : 0;
+        }
+        int rank = incl - pc;
+        const float scale = exp2i((int)st[kDataBytes + w] - 127);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const uint32_t byte = (uint32_t)(word >> (56 - 8 * c)) & 0xffu;
+          const int al = rank & ~7;
+          const uint64_t c0 = *(const uint64_t*)(st + al);
+          const uint64_t c1 = *(const uint64_t*)(st + al + 8);
+          const int sh = 8 * (rank & 7);
+          const uint64_t run = sh ? (c0 >> sh) | (c1 << (64 - sh)) : c0;
+          const uint64_t sel = sm.sel[byte];
+          const uint32_t lo = __builtin_amdgcn_perm((uint32_t)(run >> 32), (uint32_t)run, (uint32_t)sel);
+          const uint32_t hi = __builtin_amdgcn_perm((uint32_t)(run >> 32), (uint32_t)run, (uint32_t)(sel >> 32));
+          rank += __popc(byte);
+          u32x4 v = {cvt2<false>(lo, scale), cvt2<true>(lo, scale), cvt2<false>(hi, scale),
+                     cvt2<true>(hi, scale)};
+          if (w == 7 && a.freqs) {  // tail: rotate BF16 pairs with the record's RoPE row
+            const f32x4 f0 = *(const f32x4*)(sm.freq + r * 64 + 8 * c);
+            const f32x4 f1 = *(const f32x4*)(sm.freq + r * 64 + 8 * c + 4);
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              x[2 * i] = u2f(v[i] << 16);
+              x[2 * i + 1] = u2f(v[i] & 0xffff0000u);
+            }
+            float cs[8] = {f0[0], f0[1], f0[2], f0[3], f1[0], f1[1], f1[2], f1[3]};
+            rope4(x, cs);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+          }
+          *(u32x4*)(krow + 8 * c) = v;
+        }
+      } else {
+        const float scale = w < 7 ? exp2i((int)st[kNativeDataBytes + w] - 127) : 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          u32x4 v;
+          if (w < 7) {
+            const u32x2 codes = *(const u32x2*)(st + 64 * w + 8 * c);
+            v = u32x4{cvt2<false>(codes[0], scale), cvt2<true>(codes[0], scale),
+                      cvt2<false>(codes[1], scale), cvt2<true>(codes[1], scale)};
+          } else {
+            v = *(const u32x4*)(st + kNopeDim + 16 * c);
+          }
+          *(u32x4*)(krow + 8 * c) = v;
+        }
+      }
+    }
+    __syncthreads();  // K tile ready; staging free
+    if (base + kT < n) store_tile();
+
+    // validity of the tile's records as a bit mask (records >= n are invalid)
+    const int my = base + (lane & 31);
+    const uint32_t vmask =
+        (uint32_t)__ballot((lane < 32) && my < n && sm.rec[my < n ? my : 0] >= 0);
+
+    // ---- QK partial over this wave's coordinate quarter ----
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 kv = __builtin_bit_cast(
+            bf16x8, *(const u32x4*)(sm.kd + (16 * rb + col) * kKdStride + 128 * wave + 32 * ks + 8 * g));
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qreg[ks], s, 0, 0, 0);
+      }
+      sm.spart[wave][rb][lane] = s;
+    }
+    __syncthreads();  // partial S ready
+
+    // ---- online softmax: lane holds records {rb*16 + 4g + i} for head col ----
+    float sv[8];
     float mt = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool v = (vmask >> (4 * g + i)) & 1u;
-      sv[i] = v ? s[i] * a.scale_log2 : -INFINITY;
-      mt = fmaxf(mt, sv[i]);
+    for (int rb = 0; rb < 2; ++rb) {
+      const f32x4 s = sm.spart[0][rb][lane] + sm.spart[1][rb][lane] + sm.spart[2][rb][lane] +
+                      sm.spart[3][rb][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool v = (vmask >> (16 * rb + 4 * g + i)) & 1u;
+        sv[4 * rb + i] = v ? s[i] * a.scale_log2 : -INFINITY;
+        mt = fmaxf(mt, sv[4 * rb + i]);
+      }
     }
     mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     const float m_new = fmaxf(m_run, mt);
     const float alpha = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
-    float p[4], psum = 0.0f;
+    float p[8], psum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 8; ++i) {
       p[i] = m_new == -INFINITY ? 0.0f : exp2f(sv[i] - m_new);
       psum += p[i];
     }
@@ -239,28 +343,36 @@ __global__ __launch_bounds__(64) void sparse_decode_kernel(DecodeArgs a) {
     psum += __shfl_xor(psum, 32, 64);
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    // rescale O rows (heads 4g + i) by their heads' alpha
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float ai = __shfl(alpha, 4 * g + i, 64);
 #pragma unroll
-      for (int nt = 0; nt < 32; ++nt) o[nt][i] *= ai;
+      for (int nt = 0; nt < 8; ++nt) o[nt][i] *= ai;
     }
 
-    // 5. O[head][coord] += P[head][rec] K[rec][coord]; P operand = S^T layout
-    s16x4 pa;
+    // ---- PV: O[head][coord] += P[head][rec] K[rec][coord] ----
+    s16x8 pa;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pa[i] = (short)bf16_rne(p[i]);
+    for (int i = 0; i < 8; ++i) pa[i] = (short)bf16_rne(p[i]);
+    const bf16x8 pab = __builtin_bit_cast(bf16x8, pa);
+    {
+      // lane (g, j) points at K[4g + j/4 (+16)][coord base + 4(j%4)]; receives
+      // K[4g + 0..3 (+16)][coord base + j] (transpose read)
+      const int j = col;
+      const uint16_t* r0 = sm.kd + (4 * g + (j >> 2)) * kKdStride + 128 * wave + 4 * (j & 3);
+      const uint16_t* r1 = r0 + 16 * kKdStride;
 #pragma unroll
-    for (int nt = 0; nt < 32; ++nt) {
-      s16x4 kb;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) kb[j] = (short)kd[(4 * g + j) * kKdStride + 16 * nt + col];
-      o[nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, kb, o[nt], 0, 0, 0);
+      for (int nt = 0; nt < 8; ++nt) {
+        const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(r0 + 16 * nt));
+        const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(r1 + 16 * nt));
+        const s16x8 bb = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+        o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, __builtin_bit_cast(bf16x8, bb), o[nt],
+                                                        0, 0, 0);
+      }
     }
-    wave_lds_sync();
+    __syncthreads();  // K tile consumed
   }
-  // lane holds O[head 4g + i][coord 16nt + col]; softmax state of head col
+  // lane holds O[head 4g + i][coord 128 wave + 16 nt + col]; softmax state of head col
 
   if (a.splits == 1) {
     const float sink2 = a.sink ? a.sink[head0 + col] * kLog2e : -INFINITY;
@@ -272,25 +384,25 @@ __global__ __launch_bounds__(64) void sparse_decode_kernel(DecodeArgs a) {
       factor = em / z;
       lse = (mz + log2f(z)) * kLn2;
     }
-    if (lane < 16) a.lse[t * a.heads + head0 + col] = lse;
+    if (wave == 0 && lane < 16) a.lse[t * a.heads + head0 + col] = lse;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float f = __shfl(factor, 4 * g + i, 64);
-      uint16_t* orow = a.out + (t * a.heads + head0 + 4 * g + i) * kHeadDim + col;
+      uint16_t* orow = a.out + (t * a.heads + head0 + 4 * g + i) * kHeadDim + 128 * wave + col;
 #pragma unroll
-      for (int nt = 0; nt < 32; ++nt) orow[16 * nt] = (uint16_t)bf16_rne(o[nt][i] * f);
+      for (int nt = 0; nt < 8; ++nt) orow[16 * nt] = (uint16_t)bf16_rne(o[nt][i] * f);
     }
   } else {
     const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     const float plse = l_run > 0.0f ? m_run + log2f(l_run) : -INFINITY;
     const int64_t slot = (t * a.splits + split) * a.heads + head0;
-    if (lane < 16) a.ws_lse[slot + col] = plse;
+    if (wave == 0 && lane < 16) a.ws_lse[slot + col] = plse;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float f = __shfl(inv, 4 * g + i, 64);
-      float* orow = a.ws_o + (slot + 4 * g + i) * kHeadDim + col;
+      float* orow = a.ws_o + (slot + 4 * g + i) * kHeadDim + 128 * wave + col;
 #pragma unroll
-      for (int nt = 0; nt < 32; ++nt) orow[16 * nt] = o[nt][i] * f;
+      for (int nt = 0; nt < 8; ++nt) orow[16 * nt] = o[nt][i] * f;
     }
   }
 }
@@ -307,24 +419,46 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   if (row >= rows) return;
   const int64_t t = row / heads, h = row - t * heads;
   const float sink2 = sink ? sink[h] * kLog2e : -INFINITY;
-  float mz = sink2;
-  for (int s = 0; s < splits; ++s) mz = fmaxf(mz, ws_lse[(t * splits + s) * heads + h]);
+  // lane s holds split s's log2-sum-exp (splits <= 64)
+  const float ls = lane < splits ? ws_lse[(t * splits + lane) * heads + h] : -INFINITY;
+  float mz = fmaxf(ls, sink2);
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) mz = fmaxf(mz, __shfl_xor(mz, d, 64));
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float lse_out = -INFINITY;
   if (mz != -INFINITY) {
-    float z = exp2f(sink2 - mz);
-    for (int s = 0; s < splits; ++s) {
-      const int64_t slot = (t * splits + s) * heads + h;
-      const float w = exp2f(ws_lse[slot] - mz);
-      z += w;
-      if (w > 0.0f) {
-        const float* src = ws_o + slot * kHeadDim + 8 * lane;
-        const f32x4 x0 = *(const f32x4*)src, x1 = *(const f32x4*)(src + 4);
+    const float w = lane < splits ? exp2f(ls - mz) : 0.0f;
+    float z = w;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) z += __shfl_xor(z, d, 64);
+    z += exp2f(sink2 - mz);
+    const float* src = ws_o + (t * splits * heads + h) * kHeadDim + 8 * lane;
+    const int64_t step = heads * kHeadDim;
+    int s = 0;
+    for (; s + 4 <= splits; s += 4) {
+      f32x4 x[8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        x[2 * u] = *(const f32x4*)(src + (s + u) * step);
+        x[2 * u + 1] = *(const f32x4*)(src + (s + u) * step + 4);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float wu = __shfl(w, s + u, 64);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          acc[i] += w * x0[i];
-          acc[4 + i] += w * x1[i];
+          acc[i] += wu * x[2 * u][i];
+          acc[4 + i] += wu * x[2 * u + 1][i];
         }
+      }
+    }
+    for (; s < splits; ++s) {
+      const float wu = __shfl(w, s, 64);
+      const f32x4 x0 = *(const f32x4*)(src + s * step), x1 = *(const f32x4*)(src + s * step + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[i] += wu * x0[i];
+        acc[4 + i] += wu * x1[i];
       }
     }
     const float inv = 1.0f / z;
@@ -344,20 +478,23 @@ struct Plan {
   size_t bytes;
 };
 
+// Aim for ~2 workgroups per CU (256 CUs); each split holds <= kMaxChunk records.
 Plan plan_for(int64_t tokens, int64_t heads, int64_t topk) {
   const int64_t base = tokens * (heads / 16);
-  const int64_t max_splits = (topk + kTile - 1) / kTile;
+  const int64_t tiles = (topk + kT - 1) / kT;
   int64_t splits = base > 0 ? (512 + base - 1) / base : 1;
-  if (splits > max_splits) splits = max_splits;
+  const int64_t min_splits = (topk + kMaxChunk - 1) / kMaxChunk;
+  if (splits > tiles) splits = tiles;
+  if (splits > kMaxSplits) splits = kMaxSplits;
+  if (splits < min_splits) splits = min_splits;
   if (splits < 1) splits = 1;
-  int64_t chunk = (topk + splits - 1) / splits;
-  chunk = (chunk + kTile - 1) / kTile * kTile;
-  if (chunk < kTile) chunk = kTile;
-  splits = (topk + chunk - 1) / chunk;
+  int64_t chunk_tiles = (tiles + splits - 1) / splits;
+  if (chunk_tiles < 1) chunk_tiles = 1;
+  splits = (tiles + chunk_tiles - 1) / chunk_tiles;
   if (splits < 1) splits = 1;
   Plan p;
   p.splits = (int)splits;
-  p.chunk = (int)chunk;
+  p.chunk = (int)(chunk_tiles * kT);
   p.bytes = splits > 1 ? (size_t)(tokens * splits * heads) * (kHeadDim + 1) * sizeof(float) : 0;
   return p;
 }
@@ -377,6 +514,8 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   const int64_t tokens = batch * q_len;
   if (tokens == 0 || heads == 0) return RM_OK;
   if (heads < 0 || heads % 16 || heads > 1024 || bt_stride < max_blocks) return RM_ERR_SHAPE;
+  if (topk > (int64_t)kMaxChunk * kMaxSplits) return RM_ERR_SHAPE;
+  if (pool_pages > ((int64_t)1 << 25)) return RM_ERR_SHAPE;  // slots fit in int32
   if (!q || !out || !lse || (topk > 0 && (!indices || !pool || !block_table)))
     return RM_ERR_NULL;
   if (!aligned(q, 16) || !aligned(out, 16) || (pool && !aligned(pool, 16)) ||
@@ -413,7 +552,7 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(sparse_decode_kernel<kPacked>,
                      dim3((unsigned)plan.splits, (unsigned)tokens, (unsigned)(heads / 16)),
-                     dim3(64), 0, s, a);
+                     dim3(kThreads), 0, s, a);
   if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   if (plan.splits > 1) {
     const int64_t rows = tokens * heads;
@@ -428,7 +567,9 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
 
 extern "C" int rm_sparse_decode_workspace(int64_t tokens, int64_t heads, int64_t topk,
                                           int32_t* num_splits, size_t* workspace_bytes) {
-  if (tokens < 0 || heads < 0 || heads % 16 || topk < 0) return RM_ERR_SHAPE;
+  if (tokens < 0 || heads < 0 || heads % 16 || topk < 0 ||
+      topk > (int64_t)kMaxChunk * kMaxSplits)
+    return RM_ERR_SHAPE;
   const Plan p = plan_for(tokens, heads, topk);
   if (num_splits) *num_splits = p.splits;
   if (workspace_bytes) *workspace_bytes = p.bytes;
@@ -460,4 +601,4 @@ extern "C" int rm_native_sparse_decode_fwd(
                               workspace_bytes, stream);
 }
 
-extern "C" int rm_version(void) { return 100; }
+extern "C" int rm_version(void) { return 200; }
