@@ -55,6 +55,8 @@ def parse():
     p.add_argument("--no-capacity", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-sample", type=int, default=196608)
+    p.add_argument("--decode-only", action="store_true",
+                   help="only the decode cases (for kernel profiling)")
     return p.parse_args()
 
 
@@ -274,6 +276,9 @@ def main():
     import remnant
     import remnant.synthetic  # noqa: F401
     torch.cuda.set_device(0)
+    if args.decode_only:
+        print(json.dumps({"decode": decode_leg(torch, remnant, args)}), flush=True)
+        return
     log(f"bulk pack + reconstruct, {args.records} records")
     b = bulk(torch, remnant, args)
     n = b["n"]

@@ -14,8 +14,8 @@
 //     whole share is resolved once into LDS;
 //   * the next tile's record bytes (and its RoPE rows) are loaded into
 //     registers while the current tile computes, then written to LDS staging;
-//   * dequantization: thread (record r, bitmap word w) expands coordinates
-//     64w..64w+63 -- v_perm places the kept E4M3 codes (zeros for pruned lanes)
+//   * dequantization: thread (record r, chunk j) expands coordinates
+//     64w+8j..64w+8j+7 of every word w -- v_perm places the kept E4M3 codes (zeros for pruned lanes)
 //     using a 256-entry selector table, v_cvt_scalef32_pk_bf16_fp8 applies the
 //     UE8M0 scale, the tail word is BF16-rounded then rotated -- into a dense
 //     BF16 tile K[32][512] in LDS;
@@ -220,50 +220,50 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
     }
   };
 
+  // prologue: tile 0 staged, tile 1 in flight
   if (n > 0) {
     load_tile(0);
     store_tile();
   }
   __syncthreads();
+  if (kT < n) load_tile(kT);
 
   for (int base = 0; base < n; base += kT) {
-    // prefetch the next tile while this one computes
-    if (base + kT < n) load_tile(base + kT);
 
-    // ---- dequantize: thread -> record tid/8, bitmap word tid%8 (64 coords) ----
+    // ---- dequantize: thread -> record tid/8, chunk j = tid%8 of every 64-coord word;
+    // the RoPE tail (word 7) is one unrolled iteration, uniform across the wave ----
     {
-      const int r = tid >> 3, w = tid & 7;
+      const int r = tid >> 3, j = tid & 7;
       const uint8_t* st = sm.stage + r * G::kStage;
-      uint16_t* krow = sm.kd + r * kKdStride + 64 * w;
+      uint16_t* krow = sm.kd + r * kKdStride + 8 * j;
       if (kPacked) {
-        const uint64_t word = *(const uint64_t*)(st + kCodeBytes + 8 * w);
-        // exclusive prefix of popcounts over the record's 8 words (lanes 8r'..8r'+7)
-        const int pc = __popcll(word);
-        int incl = pc;
+        const u32x4 b0 = *(const u32x4*)(st + kCodeBytes), b1 = *(const u32x4*)(st + kCodeBytes + 16);
+        const u32x4 b2 = *(const u32x4*)(st + kCodeBytes + 32), b3 = *(const u32x4*)(st + kCodeBytes + 48);
+        const uint64_t wd[8] = {((uint64_t)b0[1] << 32) | b0[0], ((uint64_t)b0[3] << 32) | b0[2],
+                                ((uint64_t)b1[1] << 32) | b1[0], ((uint64_t)b1[3] << 32) | b1[2],
+                                ((uint64_t)b2[1] << 32) | b2[0], ((uint64_t)b2[3] << 32) | b2[2],
+                                ((uint64_t)b3[1] << 32) | b3[0], ((uint64_t)b3[3] << 32) | b3[2]};
+        const u32x2 sb = *(const u32x2*)(st + kDataBytes);
+        const uint64_t before = ~(~0ull >> (8 * j));  // coordinates of earlier chunks in a word
+        int base_rank = 0;
 #pragma unroll
-        for (int d = 1; d < 8; d <<= 1) {
-          const int up = __shfl_up(incl, d, 8);
-          incl += (w >= d) ? up : 0;
-        }
-        int rank = incl - pc;
-        const float scale = exp2i((int)st[kDataBytes + w] - 127);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const uint32_t byte = (uint32_t)(word >> (56 - 8 * c)) & 0xffu;
-          const int al = rank & ~7;
-          const uint64_t c0 = *(const uint64_t*)(st + al);
-          const uint64_t c1 = *(const uint64_t*)(st + al + 8);
-          const int sh = 8 * (rank & 7);
-          const uint64_t run = sh ? (c0 >> sh) | (c1 << (64 - sh)) : c0;
+        for (int w = 0; w < 8; ++w) {
+          const uint32_t byte = (uint32_t)(wd[w] >> (56 - 8 * j)) & 0xffu;
+          const int rank = base_rank + __popcll(wd[w] & before);
+          base_rank += __popcll(wd[w]);
+          const uint32_t* cw = (const uint32_t*)(st + (rank & ~3));
+          const uint32_t d0 = cw[0], d1 = cw[1], d2 = cw[2];
+          const uint32_t lo4 = __builtin_amdgcn_alignbyte(d1, d0, (uint32_t)rank & 3u);
+          const uint32_t hi4 = __builtin_amdgcn_alignbyte(d2, d1, (uint32_t)rank & 3u);
           const uint64_t sel = sm.sel[byte];
-          const uint32_t lo = __builtin_amdgcn_perm((uint32_t)(run >> 32), (uint32_t)run, (uint32_t)sel);
-          const uint32_t hi = __builtin_amdgcn_perm((uint32_t)(run >> 32), (uint32_t)run, (uint32_t)(sel >> 32));
-          rank += __popc(byte);
+          const uint32_t lo = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)sel);
+          const uint32_t hi = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)(sel >> 32));
+          const float scale = exp2i((int)((sb[w >> 2] >> (8 * (w & 3))) & 0xffu) - 127);
           u32x4 v = {cvt2<false>(lo, scale), cvt2<true>(lo, scale), cvt2<false>(hi, scale),
                      cvt2<true>(hi, scale)};
           if (w == 7 && a.freqs) {  // tail: rotate BF16 pairs with the record's RoPE row
-            const f32x4 f0 = *(const f32x4*)(sm.freq + r * 64 + 8 * c);
-            const f32x4 f1 = *(const f32x4*)(sm.freq + r * 64 + 8 * c + 4);
+            const f32x4 f0 = *(const f32x4*)(sm.freq + r * 64 + 8 * j);
+            const f32x4 f1 = *(const f32x4*)(sm.freq + r * 64 + 8 * j + 4);
             float x[8];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -275,26 +275,26 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
           }
-          *(u32x4*)(krow + 8 * c) = v;
+          *(u32x4*)(krow + 64 * w) = v;
         }
       } else {
-        const float scale = w < 7 ? exp2i((int)st[kNativeDataBytes + w] - 127) : 0.0f;
+        const u32x2 sb = *(const u32x2*)(st + kNativeDataBytes);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int w = 0; w < 8; ++w) {
           u32x4 v;
           if (w < 7) {
-            const u32x2 codes = *(const u32x2*)(st + 64 * w + 8 * c);
+            const float scale = exp2i((int)((sb[w >> 2] >> (8 * (w & 3))) & 0xffu) - 127);
+            const u32x2 codes = *(const u32x2*)(st + 64 * w + 8 * j);
             v = u32x4{cvt2<false>(codes[0], scale), cvt2<true>(codes[0], scale),
                       cvt2<false>(codes[1], scale), cvt2<true>(codes[1], scale)};
           } else {
-            v = *(const u32x4*)(st + kNopeDim + 16 * c);
+            v = *(const u32x4*)(st + kNopeDim + 16 * j);
           }
-          *(u32x4*)(krow + 8 * c) = v;
+          *(u32x4*)(krow + 64 * w) = v;
         }
       }
     }
     __syncthreads();  // K tile ready; staging free
-    if (base + kT < n) store_tile();
 
     // validity of the tile's records as a bit mask (records >= n are invalid)
     const int my = base + (lane & 31);
@@ -343,11 +343,13 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
     psum += __shfl_xor(psum, 32, 64);
     l_run = l_run * alpha + psum;
     m_run = m_new;
+    if (__ballot(alpha != 1.0f)) {  // some head's running max moved: rescale O
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float ai = __shfl(alpha, 4 * g + i, 64);
+      for (int i = 0; i < 4; ++i) {
+        const float ai = __shfl(alpha, 4 * g + i, 64);
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) o[nt][i] *= ai;
+        for (int nt = 0; nt < 8; ++nt) o[nt][i] *= ai;
+      }
     }
 
     // ---- PV: O[head][coord] += P[head][rec] K[rec][coord] ----
@@ -370,7 +372,11 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
                                                         0, 0, 0);
       }
     }
-    __syncthreads();  // K tile consumed
+    // the next tile's bytes were requested one iteration ago: stage them, then
+    // request the tile after it so its latency overlaps a whole iteration
+    if (base + kT < n) store_tile();
+    if (base + 2 * kT < n) load_tile(base + 2 * kT);
+    __syncthreads();  // K tile consumed; next tile staged
   }
   // lane holds O[head 4g + i][coord 128 wave + 16 nt + col]; softmax state of head col
 
@@ -407,69 +413,68 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
   }
 }
 
-// Merge split partials with the sink: one wave per (token, head), 8 coords/lane.
+// Merge split partials with the sink. One workgroup (4 waves) per (token,
+// head) row: wave w takes splits w, w+4, ...; lane l owns coordinates
+// 8l..8l+7; the 4 partial sums meet in LDS in a fixed order.
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ ws_o,
                                                       const float* __restrict__ ws_lse,
                                                       const float* __restrict__ sink, int splits,
-                                                      int64_t heads, int64_t rows,
-                                                      uint16_t* __restrict__ out,
+                                                      int64_t heads, uint16_t* __restrict__ out,
                                                       float* __restrict__ lse) {
+  __shared__ f32x4 part[4][2][64];
   const int lane = wave_lane();
-  const int64_t row = (int64_t)blockIdx.x * 4 + uniform((int)(threadIdx.x >> 6));
-  if (row >= rows) return;
+  const int wave = uniform((int)(threadIdx.x >> 6));
+  const int64_t row = blockIdx.x;
   const int64_t t = row / heads, h = row - t * heads;
   const float sink2 = sink ? sink[h] * kLog2e : -INFINITY;
-  // lane s holds split s's log2-sum-exp (splits <= 64)
+  // every wave reads all split LSEs (lane s holds split s; splits <= 64)
   const float ls = lane < splits ? ws_lse[(t * splits + lane) * heads + h] : -INFINITY;
   float mz = fmaxf(ls, sink2);
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) mz = fmaxf(mz, __shfl_xor(mz, d, 64));
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float lse_out = -INFINITY;
-  if (mz != -INFINITY) {
-    const float w = lane < splits ? exp2f(ls - mz) : 0.0f;
-    float z = w;
+  const float w = (mz != -INFINITY && lane < splits) ? exp2f(ls - mz) : 0.0f;
+  float z = w;
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) z += __shfl_xor(z, d, 64);
-    z += exp2f(sink2 - mz);
-    const float* src = ws_o + (t * splits * heads + h) * kHeadDim + 8 * lane;
-    const int64_t step = heads * kHeadDim;
-    int s = 0;
-    for (; s + 4 <= splits; s += 4) {
-      f32x4 x[8];
+  for (int d = 1; d < 64; d <<= 1) z += __shfl_xor(z, d, 64);
+  const float* src = ws_o + (t * splits * heads + h) * kHeadDim + 8 * lane;
+  const int64_t step = heads * kHeadDim;
+  f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+  constexpr int kU = 4;  // splits per batch of in-flight loads, per wave
+  for (int s0 = wave; s0 < splits; s0 += 4 * kU) {
+    f32x4 x[2 * kU];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        x[2 * u] = *(const f32x4*)(src + (s + u) * step);
-        x[2 * u + 1] = *(const f32x4*)(src + (s + u) * step + 4);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float wu = __shfl(w, s + u, 64);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[i] += wu * x[2 * u][i];
-          acc[4 + i] += wu * x[2 * u + 1][i];
-        }
-      }
+    for (int u = 0; u < kU; ++u) {
+      const int s = s0 + 4 * u;
+      x[2 * u] = s < splits ? *(const f32x4*)(src + s * step) : f32x4{0.f, 0.f, 0.f, 0.f};
+      x[2 * u + 1] = s < splits ? *(const f32x4*)(src + s * step + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    for (; s < splits; ++s) {
-      const float wu = __shfl(w, s, 64);
-      const f32x4 x0 = *(const f32x4*)(src + s * step), x1 = *(const f32x4*)(src + s * step + 4);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[i] += wu * x0[i];
-        acc[4 + i] += wu * x1[i];
-      }
+    for (int u = 0; u < kU; ++u) {
+      const int s = s0 + 4 * u;
+      const float wu = __shfl(w, s < splits ? s : 0, 64);
+      const float ww = s < splits ? wu : 0.0f;
+      a0 += ww * x[2 * u];
+      a1 += ww * x[2 * u + 1];
     }
-    const float inv = 1.0f / z;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] *= inv;
-    lse_out = (mz + log2f(z)) * kLn2;
   }
-  *(u32x4*)(out + row * kHeadDim + 8 * lane) =
-      u32x4{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]), pack_bf16x2(acc[4], acc[5]),
-            pack_bf16x2(acc[6], acc[7])};
-  if (lane == 0) lse[row] = lse_out;
+  part[wave][0][lane] = a0;
+  part[wave][1][lane] = a1;
+  __syncthreads();
+  if (wave == 0) {
+    float lse_out = -INFINITY;
+    f32x4 r0 = {0.f, 0.f, 0.f, 0.f}, r1 = {0.f, 0.f, 0.f, 0.f};
+    if (mz != -INFINITY) {
+      const float zt = z + exp2f(sink2 - mz);
+      const float inv = 1.0f / zt;
+      r0 = (part[0][0][lane] + part[1][0][lane] + part[2][0][lane] + part[3][0][lane]) * inv;
+      r1 = (part[0][1][lane] + part[1][1][lane] + part[2][1][lane] + part[3][1][lane]) * inv;
+      lse_out = (mz + log2f(zt)) * kLn2;
+    }
+    *(u32x4*)(out + row * kHeadDim + 8 * lane) =
+        u32x4{pack_bf16x2(r0[0], r0[1]), pack_bf16x2(r0[2], r0[3]), pack_bf16x2(r1[0], r1[1]),
+              pack_bf16x2(r1[2], r1[3])};
+    if (lane == 0) lse[row] = lse_out;
+  }
 }
 
 struct Plan {
@@ -556,8 +561,8 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   if (plan.splits > 1) {
     const int64_t rows = tokens * heads;
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s,
-                       a.ws_o, a.ws_lse, sink, plan.splits, heads, rows, out, lse);
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)rows), dim3(256), 0, s, a.ws_o, a.ws_lse,
+                       sink, plan.splits, heads, out, lse);
     if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   }
   return RM_OK;
