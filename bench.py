@@ -57,6 +57,8 @@ def parse():
     p.add_argument("--cpu-sample", type=int, default=196608)
     p.add_argument("--decode-only", action="store_true",
                    help="only the decode cases (for kernel profiling)")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="also run a plain 512 MiB device copy (counter calibration)")
     return p.parse_args()
 
 
@@ -298,6 +300,13 @@ def main():
     dom_bytes = n * (PACK_BYTES if dominant == "pack" else RECON_BYTES)
     achieved = dom_bytes / (dom_ms * 1e6)
     traffic = load_traffic().get(dominant)
+    if args.copy_probe:
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     line = {
         "metric": METRIC,
         "value": n / (ms_per_step * 1e-3),

@@ -72,12 +72,18 @@ struct DecodeArgs {
   float* ws_lse;   // [tokens, splits, heads]
 };
 
+// Staging geometry. A Packed record (328 B, 8-byte aligned) is fetched as the 21
+// aligned 16-byte pieces covering it (the last piece shrinks to 8 bytes when
+// the record is 16-byte aligned, so nothing past the record is read) and
+// written to its 336-byte staging row shifted so the record starts at offset 0. A Native record stages
+// its 576-byte data row (36 pieces) plus its 8-byte scale row.
 template <bool kPacked>
 struct Geo {
-  static constexpr int kData = kPacked ? kDataBytes : kNativeDataBytes;
+  static constexpr int kData = kPacked ? kRecordBytes : kNativeDataBytes;  // row pitch
   static constexpr int kPage = kPacked ? kPageBytes : kNativePageBytes;
-  static constexpr int kStage = kData + 16;             // data row + 8 scale bytes + pad
-  static constexpr int kDataChunks = kT * kData / 16;   // 16-byte pieces per tile
+  static constexpr int kPieces = kPacked ? 21 : kNativeDataBytes / 16;
+  static constexpr int kStage = kPacked ? 336 : kNativeDataBytes + 16;
+  static constexpr int kDataChunks = kT * kPieces;      // 16-byte pieces per tile
   static constexpr int kDataLoads = (kDataChunks + kThreads - 1) / kThreads;
   static constexpr int kFreqLoads = kPacked ? (kT * 256 / 16) / kThreads : 0;  // 2
 };
@@ -165,22 +171,34 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
   u32x4 pre[G::kDataLoads];
   u32x2 pre_scale;
   u32x4 pre_freq[G::kFreqLoads > 0 ? G::kFreqLoads : 1];
+  int base_next = 0;  // first record of the tile held in the prefetch registers
   auto load_tile = [&](int base) {
+    base_next = base;
 #pragma unroll
     for (int j = 0; j < G::kDataLoads; ++j) {
       const int c = tid + j * kThreads;
       pre[j] = u32x4{0u, 0u, 0u, 0u};
       if (c < G::kDataChunks) {
-        const int r = c / (G::kData / 16), piece = c % (G::kData / 16);
+        const int r = c / G::kPieces, piece = c % G::kPieces;
         const int slot = base + r < n ? sm.rec[base + r] : -1;
         if (slot >= 0) {
-          const uint8_t* page = a.pool + (int64_t)(slot >> 6) * G::kPage;
-          pre[j] = *(const u32x4*)(page + (slot & 63) * G::kData + 16 * piece);
+          const uint8_t* row = a.pool + (int64_t)(slot >> 6) * G::kPage + (slot & 63) * G::kData;
+          if (kPacked) {
+            const uint8_t* al = row - 8 * (slot & 1);  // odd rows start 8 bytes past 16
+            if (piece == G::kPieces - 1 && !(slot & 1)) {
+              const u32x2 t8 = *(const u32x2*)(al + 16 * piece);
+              pre[j] = u32x4{t8[0], t8[1], 0u, 0u};
+            } else {
+              pre[j] = *(const u32x4*)(al + 16 * piece);
+            }
+          } else {
+            pre[j] = *(const u32x4*)(row + 16 * piece);
+          }
         }
       }
     }
     pre_scale = u32x2{0u, 0u};
-    if (tid < kT) {
+    if (!kPacked && tid < kT) {
       const int slot = base + tid < n ? sm.rec[base + tid] : -1;
       if (slot >= 0) {
         const uint8_t* page = a.pool + (int64_t)(slot >> 6) * G::kPage;
@@ -206,11 +224,24 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
     for (int j = 0; j < G::kDataLoads; ++j) {
       const int c = tid + j * kThreads;
       if (c < G::kDataChunks) {
-        const int r = c / (G::kData / 16), piece = c % (G::kData / 16);
-        *(u32x4*)(sm.stage + r * G::kStage + 16 * piece) = pre[j];
+        const int r = c / G::kPieces, piece = c % G::kPieces;
+        uint8_t* dst = sm.stage + r * G::kStage + 16 * piece;
+        if (kPacked) {
+          // odd pool rows were fetched from 8 bytes before the record: shift them
+          // down so every staged record starts at offset 0
+          const int slot = base_next + r < n ? sm.rec[base_next + r] : 0;
+          if (slot & 1) {
+            if (piece > 0) *(u32x2*)(dst - 8) = u32x2{pre[j][0], pre[j][1]};
+            *(u32x2*)dst = u32x2{pre[j][2], pre[j][3]};
+          } else {
+            *(u32x4*)dst = pre[j];
+          }
+        } else {
+          *(u32x4*)dst = pre[j];
+        }
       }
     }
-    if (tid < kT) *(u32x2*)(sm.stage + tid * G::kStage + G::kData) = pre_scale;
+    if (!kPacked && tid < kT) *(u32x2*)(sm.stage + tid * G::kStage + G::kData) = pre_scale;
     if (kPacked) {
 #pragma unroll
       for (int j = 0; j < G::kFreqLoads; ++j) {
@@ -234,15 +265,15 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
     // the RoPE tail (word 7) is one unrolled iteration, uniform across the wave ----
     {
       const int r = tid >> 3, j = tid & 7;
-      const uint8_t* st = sm.stage + r * G::kStage;
       uint16_t* krow = sm.kd + r * kKdStride + 8 * j;
       if (kPacked) {
-        const u32x4 b0 = *(const u32x4*)(st + kCodeBytes), b1 = *(const u32x4*)(st + kCodeBytes + 16);
-        const u32x4 b2 = *(const u32x4*)(st + kCodeBytes + 32), b3 = *(const u32x4*)(st + kCodeBytes + 48);
-        const uint64_t wd[8] = {((uint64_t)b0[1] << 32) | b0[0], ((uint64_t)b0[3] << 32) | b0[2],
-                                ((uint64_t)b1[1] << 32) | b1[0], ((uint64_t)b1[3] << 32) | b1[2],
-                                ((uint64_t)b2[1] << 32) | b2[0], ((uint64_t)b2[3] << 32) | b2[2],
-                                ((uint64_t)b3[1] << 32) | b3[0], ((uint64_t)b3[3] << 32) | b3[2]};
+        const uint8_t* st = sm.stage + r * G::kStage;
+        uint64_t wd[8];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          const u32x2 v = *(const u32x2*)(st + kCodeBytes + 8 * w);
+          wd[w] = ((uint64_t)v[1] << 32) | v[0];
+        }
         const u32x2 sb = *(const u32x2*)(st + kDataBytes);
         const uint64_t before = ~(~0ull >> (8 * j));  // coordinates of earlier chunks in a word
         int base_rank = 0;
@@ -278,6 +309,7 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
           *(u32x4*)(krow + 64 * w) = v;
         }
       } else {
+        const uint8_t* st = sm.stage + r * G::kStage;
         const u32x2 sb = *(const u32x2*)(st + kNativeDataBytes);
 #pragma unroll
         for (int w = 0; w < 8; ++w) {

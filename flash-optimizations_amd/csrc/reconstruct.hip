@@ -38,11 +38,16 @@ __device__ __forceinline__ void expand8(uint32_t bits, uint64_t run, float scale
 __device__ __forceinline__ void dequant_lane(const uint8_t* __restrict__ data,
                                              const uint8_t* __restrict__ scales, int lane,
                                              float* v) {
-  // Bitmap words as little-endian 64-bit values; word w covers coords 64w..64w+63.
-  const u32x4* bm = (const u32x4*)(data + kCodeBytes);
-  u32x4 b0 = bm[0], b1 = bm[1], b2 = bm[2], b3 = bm[3];
-  uint32_t wlo[8] = {b0[0], b0[2], b1[0], b1[2], b2[0], b2[2], b3[0], b3[2]};
-  uint32_t whi[8] = {b0[1], b0[3], b1[1], b1[3], b2[1], b2[3], b3[1], b3[3]};
+  // Bitmap words as little-endian 64-bit values; word w covers coords 64w..64w+63
+  // (records are 8-byte aligned, so the words are read as 8-byte loads).
+  const u32x2* bm = (const u32x2*)(data + kCodeBytes);
+  uint32_t wlo[8], whi[8];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    const u32x2 v = bm[w];
+    wlo[w] = v[0];
+    whi[w] = v[1];
+  }
   const int word = lane >> 3, sub = lane & 7;
   int rank = 0;
   uint64_t mine = 0;
@@ -84,11 +89,9 @@ __global__ __launch_bounds__(256) void unpack_gather_kernel(
     }
     u32x4 o = {0u, 0u, 0u, 0u};
     if (valid) {
-      const uint8_t* page = pool + (p >> 6) * kPageBytes;
-      const int slot = (int)(p & 63);
+      const uint8_t* rec = pool + (p >> 6) * kPageBytes + (p & 63) * kRecordBytes;
       float v[8];
-      dequant_lane(page + slot * kDataBytes, page + kPageRecords * kDataBytes + slot * kScaleBytes,
-                   lane, v);
+      dequant_lane(rec, rec + kDataBytes, lane, v);
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = bf16_to_f32(bf16_rne(v[i]));
       if (freqs && lane >= kNopeDim / 8) {

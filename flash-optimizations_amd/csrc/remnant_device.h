@@ -3,11 +3,11 @@
 //
 // Record geometry (docs/agents/numerical-and-validation.md:10-12 in the
 // reference): 512 coordinates = 448 NoPE + 64 RoPE tail; Packed keeps 256 as
-// E4M3 codes + a 512-bit bitmap + 8 UE8M0 scales = 328 bytes. A page holds 64
-// records: the 64 data rows (codes, then bitmap; 320 bytes) followed by the 64
-// scale rows (8 bytes), so every data row starts on a 16-byte boundary.
-// Native records are 584 bytes: 448 E4M3 codes + 64 rotated BF16 + 8 scales,
-// paged the same way (576-byte data rows, then 8-byte scale rows).
+// E4M3 codes + a 512-bit bitmap + 8 UE8M0 scales = 328 bytes, stored as one
+// contiguous record (codes, bitmap, scales); a page holds 64 records, so a
+// record starts 16-byte aligned (even rows) or 8 bytes past it (odd rows).
+// Native records are 584 bytes: 448 E4M3 codes + 64 rotated BF16 + 8 scales; a
+// Native page keeps its 64 data rows (576 bytes) followed by the 64 scale rows.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -23,8 +23,9 @@ constexpr int kCodeBytes = 256;
 constexpr int kBitmapBytes = 64;
 constexpr int kDataBytes = kCodeBytes + kBitmapBytes;   // 320
 constexpr int kScaleBytes = 8;
+constexpr int kRecordBytes = kDataBytes + kScaleBytes;                        // 328
 constexpr int kPageRecords = 64;
-constexpr int kPageBytes = kPageRecords * (kDataBytes + kScaleBytes);        // 20992
+constexpr int kPageBytes = kPageRecords * kRecordBytes;                       // 20992
 constexpr int kNativeDataBytes = kNopeDim + 2 * (kHeadDim - kNopeDim);       // 576
 constexpr int kNativePageBytes = kPageRecords * (kNativeDataBytes + kScaleBytes);  // 37376
 

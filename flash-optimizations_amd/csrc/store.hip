@@ -175,14 +175,9 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     if ((lane & 7) == 0) st[kDataBytes + (lane >> 3)] = (uint8_t)(e + 127);
     wave_lds_sync();
 
-    uint8_t* page = pool + (slot >> 6) * kPageBytes;
-    const int row = (int)(slot & 63);
-    if (lane < kDataBytes / 16) {
-      *(u32x4*)(page + row * kDataBytes + 16 * lane) = *(const u32x4*)(st + 16 * lane);
-    } else if (lane == kDataBytes / 16) {
-      *(u32x2*)(page + kPageRecords * kDataBytes + row * kScaleBytes) =
-          *(const u32x2*)(st + kDataBytes);
-    }
+    // the 328-byte record is 8-byte aligned: 41 lanes store 8 bytes each
+    uint8_t* dst = pool + (slot >> 6) * kPageBytes + (slot & 63) * kRecordBytes;
+    if (lane < kRecordBytes / 8) *(u32x2*)(dst + 8 * lane) = *(const u32x2*)(st + 8 * lane);
     wave_lds_sync();
   }
 }

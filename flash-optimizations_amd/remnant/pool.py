@@ -5,12 +5,14 @@ Packed planes ``values`` u8 [rows, 256], ``bitmaps`` u64 [rows, 8] and
 ``scales`` u8 [rows, 8] (candidate-sglang.patch:900-904) in pages of 64 C4
 records (decode-store timing.json ``page_size: 64``).
 
-MI355X layout: one contiguous uint8 buffer [layers, pages, page_bytes]. A page
-keeps its 64 data rows (codes + bitmap, 320 B each, every row 16-byte aligned)
-followed by its 64 scale rows (8 B), so a record's hot bytes are one aligned
-320-byte span for 16-byte vector loads. The three reference planes are exposed
-as strided views of the same memory (no copies), which is what a host-cache
-transfer or an inspection needs.
+MI355X layout: one contiguous uint8 buffer [layers, pages, page_bytes]. A
+Packed page holds 64 contiguous 328-byte records (256 codes, 64 bitmap bytes,
+8 scales), so a gathered record is one 328-byte span touching as few HBM
+lines as its size allows. A Native page keeps the reference's layout: 64 data
+rows of 576 bytes, then 64 scale rows of 8 bytes (the tail read
+``native[page, value_base + 448 : value_base + 576]``, candidate-sglang.patch:701). The reference's planes are exposed as strided views of the
+same memory (no copies), which is what a host-cache transfer or an inspection
+needs.
 """
 
 from __future__ import annotations
@@ -52,11 +54,19 @@ class LatentPool:
         return self.buffer[0 if layer_id is None else layer_id]
 
     def _data_rows(self, layer_id):
+        if self.packed:  # contiguous records: data = first 320 bytes of each
+            pg = self.layer(layer_id).reshape(self.pages, config.PAGE_RECORDS,
+                                              config.PACKED_RECORD_BYTES)
+            return pg[..., : self.data_bytes]
         pg = self.layer(layer_id)[:, : config.PAGE_RECORDS * self.data_bytes]
         return pg.reshape(self.pages, config.PAGE_RECORDS, self.data_bytes)
 
     def scales(self, layer_id: int | None = None) -> torch.Tensor:
         """Scale plane view [pages, 64, 8] u8."""
+        if self.packed:
+            pg = self.layer(layer_id).reshape(self.pages, config.PAGE_RECORDS,
+                                              config.PACKED_RECORD_BYTES)
+            return pg[..., self.data_bytes:]
         pg = self.layer(layer_id)[:, config.PAGE_RECORDS * self.data_bytes:]
         return pg.reshape(self.pages, config.PAGE_RECORDS, 8)
 

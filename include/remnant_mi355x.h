@@ -7,10 +7,10 @@
  * argument; nothing was launched). Empty inputs return RM_OK without a launch.
  *
  * Pool geometry (identical for every entry point):
- *   Packed page (20,992 B) = 64 data rows of 320 B (256 E4M3 codes in ascending
- *   coordinate order, then 8 little-endian uint64 bitmap words, MSB-first:
- *   coordinate c is bit 63 - c % 64 of word c / 64) followed by 64 scale rows
- *   of 8 UE8M0 bytes. Logical record size 328 B.
+ *   Packed page (20,992 B) = 64 contiguous 328-byte records: 256 E4M3 codes in
+ *   ascending coordinate order, then 8 little-endian uint64 bitmap words
+ *   (MSB-first: coordinate c is bit 63 - c % 64 of word c / 64), then 8 UE8M0
+ *   scale bytes (one per 64-coordinate group). Records are 8-byte aligned.
  *   Native page (37,376 B) = 64 data rows of 576 B (448 E4M3 codes, 64 rotated
  *   BF16) followed by 64 scale rows (7 UE8M0 bytes + 1 zero byte). 584 B/record.
  *   Pool slot s lives in page s / 64, row s % 64.

@@ -29,8 +29,10 @@
  *     (distance 1, 2, 4, ... 32);
  *   - rsqrt(v) = RN(1 / RN(sqrt(v))); (m * r) * w are two rounded products;
  *   - bitmap words are MSB-first: coordinate c is bit 63 - (c % 64) of word c/64;
- *   - a page of 64 records stores the 64 data rows (codes then bitmap,
- *     320 bytes each) followed by the 64 scale rows (8 bytes each);
+ *   - a Packed page holds 64 contiguous 328-byte records (codes, bitmap,
+ *     scales); a Native page holds the 64 data rows (576 bytes) followed by
+ *     the 64 scale rows (8 bytes), matching the reference's Native tail read
+ *     native[page, value_base + 448 : value_base + 576] (candidate-sglang.patch:701);
  *   - the RoPE pair rotation is re = RN(RN(xr*c) - RN(xi*s)),
  *     im = RN(RN(xr*s) + RN(xi*c)), on BF16-rounded inputs.
  */
@@ -49,8 +51,9 @@
 #define BITMAP_BYTES 64
 #define DATA_BYTES 320  /* codes + bitmap */
 #define SCALE_BYTES 8
+#define RECORD_BYTES (DATA_BYTES + SCALE_BYTES) /* 328 */
 #define PAGE_RECORDS 64
-#define PAGE_BYTES (PAGE_RECORDS * (DATA_BYTES + SCALE_BYTES)) /* 20992 */
+#define PAGE_BYTES (PAGE_RECORDS * RECORD_BYTES) /* 20992 */
 #define NATIVE_DATA_BYTES 576 /* 448 e4m3 + 64 bf16 */
 #define NATIVE_PAGE_BYTES (PAGE_RECORDS * (NATIVE_DATA_BYTES + SCALE_BYTES))
 
@@ -220,10 +223,8 @@ void orc_pack_rows_paged(const float* x, const float* w, float eps, const int32_
     for (int64_t i = 0; i < rows; ++i) {
         int64_t s = slot[i];
         if (s < 0 || s >= pool_pages * PAGE_RECORDS) continue;
-        uint8_t* page = pool + page_of(s) * PAGE_BYTES;
-        int in = (int)(s % PAGE_RECORDS);
-        orc_pack_row(x + i * HEAD_DIM, w, eps, page + in * DATA_BYTES,
-                     page + PAGE_RECORDS * DATA_BYTES + in * SCALE_BYTES, NULL, NULL);
+        uint8_t* rec = pool + page_of(s) * PAGE_BYTES + (s % PAGE_RECORDS) * RECORD_BYTES;
+        orc_pack_row(x + i * HEAD_DIM, w, eps, rec, rec + DATA_BYTES, NULL, NULL);
     }
 }
 
@@ -270,10 +271,8 @@ void orc_unpack_gather(const uint8_t* pool, int64_t pool_pages, const int32_t* p
             int valid = k < lengths[q * ls] && p >= 0 && p < rows;
             if (freqs) valid = valid && r >= 0 && r * 4 < freq_rows;
             if (!valid) { memset(o, 0, HEAD_DIM * 2); continue; }
-            const uint8_t* page = pool + page_of(p) * PAGE_BYTES;
-            int in = (int)(p % PAGE_RECORDS);
-            orc_unpack_row(page + in * DATA_BYTES,
-                           page + PAGE_RECORDS * DATA_BYTES + in * SCALE_BYTES, o);
+            const uint8_t* rec = pool + page_of(p) * PAGE_BYTES + (p % PAGE_RECORDS) * RECORD_BYTES;
+            orc_unpack_row(rec, rec + DATA_BYTES, o);
             if (freqs) orc_rope_tail(o, freqs + r * 4 * ROPE_PAIRS * 2);
         }
 }
@@ -342,8 +341,8 @@ void orc_decode_gather(const uint8_t* pool, int64_t pool_pages, int packed,
         if (!ok) { memset(o, 0, HEAD_DIM * 2); continue; }
         int in = (int)(r % PAGE_RECORDS);
         if (packed) {
-            const uint8_t* pg = pool + page * PAGE_BYTES;
-            orc_unpack_row(pg + in * DATA_BYTES, pg + PAGE_RECORDS * DATA_BYTES + in * SCALE_BYTES, o);
+            const uint8_t* rec = pool + page * PAGE_BYTES + in * RECORD_BYTES;
+            orc_unpack_row(rec, rec + DATA_BYTES, o);
             if (freqs) orc_rope_tail(o, freqs + r * 4 * ROPE_PAIRS * 2);
         } else {
             const uint8_t* pg = pool + page * NATIVE_PAGE_BYTES;

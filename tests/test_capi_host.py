@@ -180,8 +180,9 @@ def test_pool_planes_and_capacity():
     assert rec.shape == (1, 328)
     assert torch.all(rec[0, :256] == 7) and torch.all(rec[0, 256:320] == 9)
     assert torch.all(rec[0, 320:] == 11)
-    # the data row of slot 69 starts 16-byte aligned inside its page
-    assert (5 * 320) % 16 == 0 and config.PACKED_PAGE_BYTES % 16 == 0
+    # contiguous 328-byte records: slot 69 is bytes 5*328.. of page 1
+    assert torch.equal(pool.layer()[1, 5 * 328:6 * 328], rec[0])
+    assert config.PACKED_PAGE_BYTES % 16 == 0
     hbm = 288 * 10**9
     packed, native = remnant.records_fitting(hbm, "direct"), remnant.records_fitting(hbm, "native")
     assert abs(packed / 878.0e6 - 1) < 1e-3 and abs(native / 493.2e6 - 1) < 1e-3
