@@ -21,6 +21,7 @@ using namespace rm;
 namespace {
 
 constexpr int kWaves = 4;
+constexpr int kStageSpill = 336;  // 64 scratch bytes after the staged record
 
 template <bool kBf16>
 __device__ __forceinline__ void load_row8(const void* x, int64_t row, int64_t stride,
@@ -62,40 +63,44 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
 }
 
 // Keep mask (bit i = coordinate 8*lane + i) of the 256 largest magnitudes.
+// Bit-serial radix select of the 256th largest key, fully unrolled: every step
+// compares the 8 keys of each lane against prefix|bit (one ballot per key slot,
+// popcounts on the scalar unit). `at` is the count at the last accepted step,
+// i.e. #{key >= threshold}; only when it exceeds 256 is there a boundary tie
+// to admit in coordinate order.
 template <bool kBf16>
 __device__ __forceinline__ uint32_t select_top256(const uint32_t* key) {
   constexpr int kLow = kBf16 ? 16 : 0;  // bf16 magnitudes have zero low halves
   uint32_t prefix = 0;
-  bool exact = false;
+  int at = 512;
+#pragma unroll
   for (int b = 30; b >= kLow; --b) {
-    uint32_t cand = prefix | (1u << b);
+    const uint32_t cand = prefix | (1u << b);
     int cnt = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) cnt += popc_ballot(key[i] >= cand);
-    if (cnt >= kKeep) prefix = cand;
-    if (cnt == kKeep) {  // {key >= cand} is exactly the top 256: no boundary tie
-      exact = true;
-      break;
-    }
+    const bool take = cnt >= kKeep;
+    prefix = take ? cand : prefix;
+    at = take ? cnt : at;
   }
   uint32_t keep = 0;
-  if (exact) {
+  if (at == kKeep) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) keep |= (key[i] >= prefix ? 1u : 0u) << i;
     return keep;
   }
-  // prefix is the 256th largest key; admit ties at it in coordinate order.
+  // admit the (kKeep - #{key > prefix}) lowest-coordinate ties at the threshold
   int gt = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) gt += popc_ballot(key[i] > prefix);
-  int need = kKeep - gt;
+  const int need = kKeep - gt;
   int before = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) before += lanes_below(__ballot(key[i] == prefix));
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    bool tie = key[i] == prefix;
-    bool k = key[i] > prefix || (tie && before < need);
+    const bool tie = key[i] == prefix;
+    const bool k = key[i] > prefix || (tie && before < need);
     before += tie ? 1 : 0;
     keep |= (k ? 1u : 0u) << i;
   }
@@ -107,7 +112,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     const void* __restrict__ x, int64_t stride, const float* __restrict__ weight, float eps,
     const int32_t* __restrict__ slots, int64_t n, uint8_t* __restrict__ pool,
     int64_t pool_rows) {
-  __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][336];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][kStageSpill + 64];
   const int lane = wave_lane();
   const int wave = uniform((int)(threadIdx.x >> 6));
   uint8_t* st = stage[wave];
@@ -158,16 +163,25 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     const int e = ue8m0_exponent(amax);
     const float inv = exp2i(-e);
 
-    // compaction: rank of this lane's first survivor among all survivors
+    // E4M3 codes (hardware RNE, OCP format; |n / 2^e| <= 448 so nothing saturates)
+    uint32_t code[8];
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const uint32_t pk = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+          bf16_to_f32(nb[i]) * inv, bf16_to_f32(nb[i + 1]) * inv, 0, false);
+      code[i] = pk & 0xffu;
+      code[i + 1] = (pk >> 8) & 0xffu;
+    }
+    // compaction: survivors go to [rank, rank + popcount) in coordinate order;
+    // pruned slots write to a per-lane scratch byte, so the stores are unconditional
     int rank = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) rank += lanes_below(__ballot((keep >> i) & 1u));
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      if ((keep >> i) & 1u) {
-        st[rank] = (uint8_t)e4m3_rne(bf16_to_f32(nb[i]) * inv);
-        ++rank;
-      }
+      const bool kept = (keep >> i) & 1u;
+      const int at = kept ? rank + __popc(keep & ((1u << i) - 1u)) : kStageSpill + lane;
+      st[at] = (uint8_t)code[i];
     }
     // bitmap byte: coordinate 8l+i is bit 7-i of byte 7 - l%8 of word l/8
     const uint32_t rev = __builtin_bitreverse32(keep) >> 24;
