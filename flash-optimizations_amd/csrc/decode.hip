@@ -73,9 +73,9 @@ struct DecodeArgs {
 };
 
 // Staging geometry. A Packed record (328 B, 8-byte aligned) is fetched as the 21
-// aligned 16-byte pieces covering it (the last piece shrinks to 8 bytes when
-// the record is 16-byte aligned, so nothing past the record is read) and
-// written to its 336-byte staging row shifted so the record starts at offset 0. A Native record stages
+// aligned 16-byte pieces covering it -- an even row's last piece reaches 8 bytes
+// into the next row of the same page, which always exists because row 63 is odd
+// -- and written to its 336-byte staging row shifted so the record starts at 0. A Native record stages
 // its 576-byte data row (36 pieces) plus its 8-byte scale row.
 template <bool kPacked>
 struct Geo {
@@ -178,31 +178,27 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
     for (int j = 0; j < G::kDataLoads; ++j) {
       const int c = tid + j * kThreads;
       pre[j] = u32x4{0u, 0u, 0u, 0u};
+      // the bound is wave-uniform (whole waves drop out of the last round)
       if (c < G::kDataChunks) {
         const int r = c / G::kPieces, piece = c % G::kPieces;
         const int slot = base + r < n ? sm.rec[base + r] : -1;
         if (slot >= 0) {
           const uint8_t* row = a.pool + (int64_t)(slot >> 6) * G::kPage + (slot & 63) * G::kData;
-          if (kPacked) {
-            const uint8_t* al = row - 8 * (slot & 1);  // odd rows start 8 bytes past 16
-            if (piece == G::kPieces - 1 && !(slot & 1)) {
-              const u32x2 t8 = *(const u32x2*)(al + 16 * piece);
-              pre[j] = u32x4{t8[0], t8[1], 0u, 0u};
-            } else {
-              pre[j] = *(const u32x4*)(al + 16 * piece);
-            }
-          } else {
-            pre[j] = *(const u32x4*)(row + 16 * piece);
-          }
+          // Packed: odd rows start 8 bytes past a 16-byte boundary and are fetched
+          // from 8 bytes earlier; an even row's last piece runs 8 bytes into the
+          // next row of the same page (row 63, the last, is odd): always in bounds
+          pre[j] = *(const u32x4*)(row - (kPacked ? 8 * (slot & 1) : 0) + 16 * piece);
         }
       }
     }
-    pre_scale = u32x2{0u, 0u};
-    if (!kPacked && tid < kT) {
-      const int slot = base + tid < n ? sm.rec[base + tid] : -1;
-      if (slot >= 0) {
-        const uint8_t* page = a.pool + (int64_t)(slot >> 6) * G::kPage;
-        pre_scale = *(const u32x2*)(page + kPageRecords * G::kData + (slot & 63) * kScaleBytes);
+    if (!kPacked) {
+      pre_scale = u32x2{0u, 0u};
+      if (tid < kT) {
+        const int slot = base + tid < n ? sm.rec[base + tid] : -1;
+        if (slot >= 0) {
+          const uint8_t* page = a.pool + (int64_t)(slot >> 6) * G::kPage;
+          pre_scale = *(const u32x2*)(page + kPageRecords * G::kData + (slot & 63) * kScaleBytes);
+        }
       }
     }
     if (kPacked) {
@@ -225,19 +221,19 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
       const int c = tid + j * kThreads;
       if (c < G::kDataChunks) {
         const int r = c / G::kPieces, piece = c % G::kPieces;
-        uint8_t* dst = sm.stage + r * G::kStage + 16 * piece;
+        uint8_t* st = sm.stage + r * G::kStage;
         if (kPacked) {
           // odd pool rows were fetched from 8 bytes before the record: shift them
-          // down so every staged record starts at offset 0
-          const int slot = base_next + r < n ? sm.rec[base_next + r] : 0;
-          if (slot & 1) {
-            if (piece > 0) *(u32x2*)(dst - 8) = u32x2{pre[j][0], pre[j][1]};
-            *(u32x2*)dst = u32x2{pre[j][2], pre[j][3]};
-          } else {
-            *(u32x4*)dst = pre[j];
-          }
+          // down so every staged record starts at offset 0 (the first half-piece
+          // of an odd row lands in the row's unused pad bytes 328..335)
+          const int rs = base_next + r < n ? sm.rec[base_next + r] : 0;
+          const int odd = rs & 1;
+          const int lo_at = odd ? (piece ? 16 * piece - 8 : kRecordBytes) : 16 * piece;
+          const int hi_at = 16 * piece + (odd ? 0 : 8);
+          *(u32x2*)(st + lo_at) = u32x2{pre[j][0], pre[j][1]};
+          *(u32x2*)(st + hi_at) = u32x2{pre[j][2], pre[j][3]};
         } else {
-          *(u32x4*)dst = pre[j];
+          *(u32x4*)(st + 16 * piece) = pre[j];
         }
       }
     }
@@ -261,13 +257,14 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
 
   for (int base = 0; base < n; base += kT) {
 
-    // ---- dequantize: thread -> record tid/8, chunk j = tid%8 of every 64-coord word;
-    // the RoPE tail (word 7) is one unrolled iteration, uniform across the wave ----
+    // ---- dequantize: thread (record r = tid/8, chunk j = tid%8) expands chunk j of
+    // every 64-coordinate word; the RoPE tail (word 7) is one unrolled iteration,
+    // uniform across the wave ----
     {
       const int r = tid >> 3, j = tid & 7;
+      const uint8_t* st = sm.stage + r * G::kStage;
       uint16_t* krow = sm.kd + r * kKdStride + 8 * j;
       if (kPacked) {
-        const uint8_t* st = sm.stage + r * G::kStage;
         uint64_t wd[8];
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
@@ -309,20 +306,22 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
           *(u32x4*)(krow + 64 * w) = v;
         }
       } else {
-        const uint8_t* st = sm.stage + r * G::kStage;
+        // Native: thread (r, j) converts chunk j of each NoPE word and copies
+        // tail chunk j, so every lane runs the same path
+        uint16_t* nrow = krow;
         const u32x2 sb = *(const u32x2*)(st + kNativeDataBytes);
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
+        for (int ww = 0; ww < 8; ++ww) {
           u32x4 v;
-          if (w < 7) {
-            const float scale = exp2i((int)((sb[w >> 2] >> (8 * (w & 3))) & 0xffu) - 127);
-            const u32x2 codes = *(const u32x2*)(st + 64 * w + 8 * j);
+          if (ww < 7) {
+            const float scale = exp2i((int)((sb[ww >> 2] >> (8 * (ww & 3))) & 0xffu) - 127);
+            const u32x2 codes = *(const u32x2*)(st + 64 * ww + 8 * j);
             v = u32x4{cvt2<false>(codes[0], scale), cvt2<true>(codes[0], scale),
                       cvt2<false>(codes[1], scale), cvt2<true>(codes[1], scale)};
           } else {
             v = *(const u32x4*)(st + kNopeDim + 16 * j);
           }
-          *(u32x4*)(krow + 64 * w) = v;
+          *(u32x4*)(nrow + 64 * ww) = v;
         }
       }
     }
@@ -385,10 +384,8 @@ __global__ __launch_bounds__(kThreads, 2) void sparse_decode_kernel(DecodeArgs a
     }
 
     // ---- PV: O[head][coord] += P[head][rec] K[rec][coord] ----
-    s16x8 pa;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) pa[i] = (short)bf16_rne(p[i]);
-    const bf16x8 pab = __builtin_bit_cast(bf16x8, pa);
+    const bf16x8 pab = {(__bf16)p[0], (__bf16)p[1], (__bf16)p[2], (__bf16)p[3],
+                        (__bf16)p[4], (__bf16)p[5], (__bf16)p[6], (__bf16)p[7]};
     {
       // lane (g, j) points at K[4g + j/4 (+16)][coord base + 4(j%4)]; receives
       // K[4g + 0..3 (+16)][coord base + j] (transpose read)
