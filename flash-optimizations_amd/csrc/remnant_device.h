@@ -83,10 +83,11 @@ __device__ __forceinline__ int wave_lane() { return (int)(threadIdx.x & 63u); }
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // Order LDS writes of a wave before later reads by other lanes of the same wave.
+// The fences cover LDS only, so outstanding global loads are not waited for.
 __device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
   __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
 // Tail rotation of 4 interleaved (re, im) pairs held as floats, with
