@@ -45,15 +45,53 @@ __device__ __forceinline__ void load_row8(const void* x, int64_t row, int64_t st
   }
 }
 
-// Sum over the wave in the fixed pairwise order (distance 1, 2, ..., 32).
+// Lane exchanges within rows of 16 (DPP): xor 1 and xor 2 inside quads, then
+// the mirrors, which pair each lane with one in the other half of its group of
+// 8 (16). In a butterfly reduction every lane of an aligned group already holds
+// the same value, so any partner in the other half gives the xor-partner's value.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float lane_value(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+
+// Sum over the wave in the fixed pairwise order (distance 1, 2, ..., 32):
+// level d adds the value of lane l ^ d. Addition commutes bitwise, so the
+// butterfly below yields exactly that result in every lane.
 __device__ __forceinline__ float wave_tree_sum(float p) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) p = p + __shfl_xor(p, d, 64);
-  return p;
+  p = p + dpp<kDppXor1>(p);
+  p = p + dpp<kDppXor2>(p);
+  p = p + dpp<kDppHalfMirror>(p);
+  p = p + dpp<kDppMirror>(p);
+  // rows of 16 are now uniform: levels 16 and 32 give (r0 + r1) + (r2 + r3)
+  return (lane_value(p, 0) + lane_value(p, 16)) + (lane_value(p, 32) + lane_value(p, 48));
 }
 
 __device__ __forceinline__ int popc_ballot(bool pred) {
   return __popcll(__ballot(pred));
+}
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+// Exclusive prefix sum of x over the wave's lanes (row shifts within rows of 16,
+// then row broadcasts 15 and 31).
+__device__ __forceinline__ int wave_exclusive_sum(int x) {
+  int v = x;
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false); // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false); // row_bcast:31
+  return v - x;
 }
 
 // Exclusive count of set predicates in lanes below this one.
@@ -148,40 +186,48 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     }
     const float sumsq = wave_tree_sum(p);
     const float r = __fdiv_rn(1.0f, __fsqrt_rn(sumsq * (1.0f / 512.0f) + eps));
-    uint32_t nb[8];
-    float amax = 0.0f;
+    // n = bf16(RN(RN(m * r) * w)) with the hardware round-to-nearest-even
+    // conversion (identical to the software rounding for every non-NaN input)
+    float y[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float y = m[i] * r;
-      y = y * w[i];
-      nb[i] = bf16_rne(y);
-      amax = fmaxf(amax, fabsf(bf16_to_f32(nb[i])));
+      y[i] = m[i] * r;
+      y[i] = y[i] * w[i];
     }
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    bf16x2 nb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) nb[i] = bf16x2{(__bf16)y[2 * i], (__bf16)y[2 * i + 1]};
+    // group amax: rounding is monotonic, so max |bf16(y)| = bf16(max |y|)
+    float ay = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
+    ay = fmaxf(ay, fmaxf(fmaxf(fabsf(y[4]), fabsf(y[5])), fmaxf(fabsf(y[6]), fabsf(y[7]))));
+    ay = fmaxf(ay, dpp<kDppXor1>(ay));  // max over the 8 lanes of the group
+    ay = fmaxf(ay, dpp<kDppXor2>(ay));
+    ay = fmaxf(ay, dpp<kDppHalfMirror>(ay));
+    const float amax = (float)(__bf16)ay;
     const int e = ue8m0_exponent(amax);
-    const float inv = exp2i(-e);
 
-    // E4M3 codes (hardware RNE, OCP format; |n / 2^e| <= 448 so nothing saturates)
-    uint32_t code[8];
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      const uint32_t pk = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
-          bf16_to_f32(nb[i]) * inv, bf16_to_f32(nb[i + 1]) * inv, 0, false);
-      code[i] = pk & 0xffu;
-      code[i + 1] = (pk >> 8) & 0xffu;
-    }
-    // compaction: survivors go to [rank, rank + popcount) in coordinate order;
-    // pruned slots write to a per-lane scratch byte, so the stores are unconditional
-    int rank = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rank += lanes_below(__ballot((keep >> i) & 1u));
+    // E4M3 codes = RNE(n / 2^e) by the scaled hardware conversion (identical to
+    // the software encode for every in-range BF16 input); |n / 2^e| <= 448
+    const float scale = exp2i(e);
+    s16x2 c01 = {0, 0}, c45 = {0, 0};
+    c01 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c01, nb[0], scale, false);
+    c01 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c01, nb[1], scale, true);
+    c45 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c45, nb[2], scale, false);
+    c45 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c45, nb[3], scale, true);
+    const uint32_t lo = __builtin_bit_cast(uint32_t, c01), hi = __builtin_bit_cast(uint32_t, c45);
+
+    // compaction: survivors go to [rank, rank + popcount) in coordinate order,
+    // rank = survivors in lower lanes (a wave prefix sum); pruned codes go to a
+    // per-lane spill byte past the record, so the stores are unconditional
+    const int cnt = __popc(keep);
+    uint8_t* const base = st + wave_exclusive_sum(cnt);
+    uint8_t* const spill = st + kStageSpill + lane;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const bool kept = (keep >> i) & 1u;
-      const int at = kept ? rank + __popc(keep & ((1u << i) - 1u)) : kStageSpill + lane;
-      st[at] = (uint8_t)code[i];
+      const uint32_t below = keep & ((1u << i) - 1u);  // survivors before slot i
+      uint8_t* const at = kept ? base + __popc(below) : spill;
+      *at = (uint8_t)((i < 4 ? lo : hi) >> (8 * (i & 3)));
     }
     // bitmap byte: coordinate 8l+i is bit 7-i of byte 7 - l%8 of word l/8
     const uint32_t rev = __builtin_bitreverse32(keep) >> 24;
