@@ -269,3 +269,14 @@ def test_decode_wide_score_range(packed):
     c = build_decode_case([3000, 900], q_len=1, heads=16, topk=1024, seed=15, packed=packed)
     c["q"] = (c["q"].float() * 300).to(torch.bfloat16)
     check_decode(c)
+
+
+@pytest.mark.parametrize("packed", [True, False], ids=["direct", "native"])
+def test_decode_partial_tiles_and_short_lengths(packed):
+    """Top-k of 100 (a partial three-tile group per split) with per-token
+    lengths 100, 37, 0 and 1: records past each length contribute nothing."""
+    banner(f"decode partial tiles packed={packed}")
+    c = build_decode_case([500, 300, 800, 64], q_len=1, heads=16, topk=100, seed=16,
+                          packed=packed)
+    c["lens"][:] = np.array([100, 37, 0, 1], np.int32).reshape(c["lens"].shape)
+    check_decode(c)
