@@ -54,6 +54,7 @@ constexpr float kRefSlack = 64.0f;         // log2 headroom above the reference 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 struct DecodeArgs {
@@ -124,6 +125,7 @@ struct Geo {
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) const uint32_t lds_u32;
 
 // Wait for every outstanding global load of this wave (LDS DMA included).
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0070); }
@@ -536,6 +538,497 @@ native_decode_kernel(DecodeArgs a) {
   decode_split<false>(a);
 }
 
+// ---------------------------------------------------------------------------
+// Producer/consumer decode. A workgroup of six waves owns (split, token,
+// 16-head block): four producer waves turn gathered records into dense BF16 K
+// tiles in an LDS ring, two consumer waves run S^T = K Q^T, the softmax and
+// O += P K on the matrix cores, each on alternate 16-record tiles with O in
+// accumulator registers. One workgroup barrier per stage (32 records) hands
+// the ring over: producers fill the two slots of stage s while consumers read
+// those of stage s - 1.
+//   * Each producer owns records 8p..8p+7 of every stage and runs a private
+//     copy pipeline: record rows (and, for Packed, the RoPE rows) are copied
+//     HBM -> LDS with global_load_lds three stages ahead, a fixed number of
+//     copies per stage, so its waits are compile-time vmcnt values.
+//   * Producer lane (record i = lane / 8, word w = lane % 8) expands the 64
+//     coordinates of one bitmap word: ranks from a prefix popcount over the 8
+//     lanes of the record (DPP), codes placed by v_perm selectors, scaled by
+//     v_cvt_scalef32_pk_bf16_fp8. The tail is rotated afterwards by all lanes.
+//   * Consumers read Q from LDS (as the MFMA operand), take weights against a fixed per-head
+//     reference (first valid tile's max) and merge their two (O, l, m) at the
+//     end.
+constexpr int kPcConsumers = 2;
+constexpr int kPcProducers = 4;
+constexpr int kPcThreads = 64 * (kPcConsumers + kPcProducers);
+constexpr int kPcStage = 32;               // records per stage: two 16-record tiles
+constexpr int kPcRing = 4;                 // K tile slots (two stages)
+constexpr int kPcKPitch = kHeadDim + 16;   // BF16 per K row (1056 B: rows 8 banks apart)
+constexpr int kPcMaxChunk = 512;           // records per split
+// instruction classes of __builtin_amdgcn_sched_group_barrier
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+
+template <bool kPacked>
+struct PcGeo {
+  static constexpr int kData = kPacked ? kRecordBytes : kNativeDataBytes;
+  static constexpr int kPage = kPacked ? kPageBytes : kNativePageBytes;
+  static constexpr int kPieces = kPacked ? 21 : kNativeDataBytes / 16;  // 16-B pieces per record
+  static constexpr int kPitch = 16 * kPieces;                          // staged record pitch
+  static constexpr int kRecPieces = 8 * kPieces;                       // one producer's 8 records
+  // Packed: the 8 RoPE rows follow, piece k of record r at slot 8 k + r
+  static constexpr int kFreqAt = 16 * kRecPieces;
+  static constexpr int kPieceCount = kRecPieces + (kPacked ? 8 * 16 : 0);
+  static constexpr int kCopies = (kPieceCount + 63) / 64;              // 16-B copies per stage
+  static constexpr int kScaleAt = 1024 * kCopies;                      // Native: scale rows
+  static constexpr int kBuf = kScaleAt + (kPacked ? 0 : 256);          // bytes per stage buffer
+  static constexpr int kLoads = kCopies + (kPacked ? 0 : 1);           // global loads per stage
+  static constexpr int kDepth = 4;                                     // copy ring buffers
+};
+
+// Max of x over lanes col, col + 16, col + 32, col + 48 (col = lane % 16).
+__device__ __forceinline__ float max_over_rows(float x) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = fmaxf(u2f(h[0]), u2f(h[1]));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(u2f(r[0]), u2f(r[1]));
+}
+
+template <bool kPacked>
+__device__ __forceinline__ void decode_pc(const DecodeArgs& a) {
+  using G = PcGeo<kPacked>;
+  __shared__ __attribute__((aligned(16))) uint16_t ktile[kPcRing][kT * kPcKPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t raw[kPcProducers][G::kDepth][G::kBuf];
+  __shared__ __attribute__((aligned(16))) uint64_t sel_tab[kPacked ? 256 : 1];
+  // per record slot of the split: pool row address, or (Q address | 1) for an
+  // invalid record or a slot past the end (a readable stand-in source, odd so
+  // that bit 0 marks it); Packed: RoPE row address (row 0 of the table for an
+  // invalid record, Q without a table)
+  __shared__ uint64_t row_tab[kPcMaxChunk];
+  __shared__ uint64_t aux_tab[kPacked ? kPcMaxChunk : 1];
+  __shared__ float mrg[kPcConsumers][2][16];  // consumers' (m_ref, l) per head
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = uniform(tid >> 6);
+  const int split = blockIdx.x;
+  const int64_t t = blockIdx.y;
+  const int64_t head0 = (int64_t)blockIdx.z * 16;
+  const int64_t b = t / a.q_len;
+
+  int64_t len = a.topk;
+  if (a.topk_length) {
+    const int64_t l = a.topk_length[t];
+    len = l < 0 ? 0 : (l < a.topk ? l : a.topk);
+  }
+  const int64_t k0 = (int64_t)split * a.chunk;
+  const int64_t k1 = k0 + a.chunk < len ? k0 + a.chunk : len;
+  const int n = k1 > k0 ? (int)(k1 - k0) : 0;
+  const int stages = (n + kPcStage - 1) / kPcStage;
+  const int64_t seqlen = a.seqlens ? a.seqlens[b] : INT64_MAX;
+
+  // Consumers hold Q of the 16 heads as the B operand of S^T = K Q^T:
+  // qf[ks] = Q[head lane % 16][32 ks + 8 (lane / 16) .. +7]
+  bf16x8 qf[16];
+  if (wv < kPcConsumers) {
+    const uint16_t* qh = a.q + (t * a.heads + head0 + (lane & 15)) * kHeadDim + 8 * (lane >> 4);
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) qf[ks] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qh + 32 * ks));
+  }
+
+  // ---- setup: selectors, record metadata ----
+  if (kPacked && tid < 256) {
+    const uint32_t e = tid;
+    uint32_t r = 0;
+    uint64_t sel = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool kept = (e >> (7 - i)) & 1u;
+      sel |= (uint64_t)(kept ? r : 0x0cu) << (8 * i);
+      r += kept ? 1u : 0u;
+    }
+    sel_tab[e] = sel;
+  }
+  const uint64_t stand_in = (uint64_t)a.q | 1u;
+  for (int i = tid; i < kPcMaxChunk; i += kPcThreads) {
+    bool ok = false;
+    int64_t r = 0, page = 0;
+    if (i < n) {
+      r = a.indices[t * a.topk + k0 + i];
+      ok = r >= 0 && r < seqlen && (r >> 6) < a.max_blocks;
+      page = ok ? a.block_table[b * a.bt_stride + (r >> 6)] : -1;
+      ok = ok && page >= 0 && page < a.pool_pages;
+      if (kPacked && a.freqs) ok = ok && r * 4 < a.freq_rows;
+    }
+    const uint8_t* pg = a.pool + (ok ? page : 0) * G::kPage;
+    row_tab[i] = ok ? (uint64_t)(pg + (r & 63) * G::kData) | (kPacked ? 0 : (uint64_t)(r & 63) << 58)
+                    : stand_in;
+    if (kPacked) aux_tab[i] = a.freqs ? (uint64_t)(a.freqs + (ok ? r : 0) * 4 * 64) : (uint64_t)a.q;
+  }
+  wait_vm();
+  __syncthreads();
+
+  // Overflow test on the consumers' published (reference, seen) maxima: a
+  // workgroup-uniform decision every wave takes from LDS.
+  auto redo_pass = [&](float& mtrue) {
+    const int h = lane & 15;
+    const float r0 = mrg[0][0][h], r1 = mrg[1][0][h], t0 = mrg[0][1][h], t1 = mrg[1][1][h];
+    mtrue = fmaxf(t0, t1);
+    return __ballot(t0 > r0 + kRefSlack || t1 > r1 + kRefSlack) != 0;
+  };
+
+  // The two roles run separate loops with the same barrier sequence per pass
+  // (stages + 1 ring barriers, then two around the overflow test), so consumer
+  // state (O) is never live in producers.
+  if (wv >= kPcConsumers) {
+    // ================= producer =================
+    constexpr int D = G::kDepth;
+    const int p = wv - kPcConsumers;
+    const uint8_t* const dummy = (const uint8_t*)a.q;
+    // Copies of stage s into ring buffer B: the record table entries first,
+    // then a fixed number of copies per stage. Invalid records and slots past
+    // the end copy from the stand-in (Q); the expansion masks them.
+    auto issue_stage = [&](int s, auto bufc) {
+      constexpr int B = decltype(bufc)::value;
+      const uint32_t base = lds_addr(&raw[p][B][0]);
+      const int rec0 = s * kPcStage + 8 * p;
+      uint64_t rw[G::kCopies];
+#pragma unroll
+      for (int j = 0; j < G::kCopies; ++j) {
+        const int c = lane + 64 * j;
+        const int r = c < G::kRecPieces ? c / G::kPieces : (c - G::kRecPieces) & 7;
+        const int idx = min(rec0 + r, kPcMaxChunk - 1);
+        rw[j] = c >= G::kPieceCount ? (uint64_t)a.q
+                : (kPacked && c >= G::kRecPieces) ? aux_tab[idx] : row_tab[idx];
+      }
+      uint64_t srow = 0;
+      if (!kPacked) srow = row_tab[min(rec0 + ((lane >> 1) & 7), kPcMaxChunk - 1)];
+#pragma unroll
+      for (int j = 0; j < G::kCopies; ++j) {
+        const int c = lane + 64 * j;
+        uint64_t src;
+        if (c < G::kRecPieces) {
+          const int piece = c - (c / G::kPieces) * G::kPieces;
+          src = (rw[j] & (kPacked ? ~(uint64_t)15 : kAddrMask & ~(uint64_t)15)) + 16 * piece;
+        } else {  // Packed RoPE piece (c - kRecPieces) / 8, or a filler lane
+          src = rw[j] + 16 * ((c - G::kRecPieces) >> 3);
+        }
+        dma16((const void*)src, base + 1024 * j);
+      }
+      if (!kPacked) {
+        const uint32_t rip = (uint32_t)(srow >> 58);
+        const bool ok = lane < 16 && !(srow & 1u);
+        const uint8_t* src = ok ? (const uint8_t*)(srow & kAddrMask) - rip * G::kData +
+                                      kPageRecords * G::kData + rip * kScaleBytes + 4 * (lane & 1)
+                                : dummy;
+        dma4(src, base + G::kScaleAt);
+      }
+    };
+
+    // Expand this wave's 8 records of stage s (ring buffer B) into the K ring.
+    // Lane (record i = lane % 8, word w = lane / 8) writes the 64 coordinates
+    // of bitmap word w; the eight records of one word sit 8 banks apart.
+    auto produce = [&](int s, auto bufc) {
+      constexpr int B = decltype(bufc)::value;
+      const int i = lane & 7, wd = lane >> 3;
+      const int rec = s * kPcStage + 8 * p + i;
+      const uint8_t* st = &raw[p][B][0] + i * G::kPitch;
+      uint16_t* const krow =
+          &ktile[(2 * s + (p >> 1)) % kPcRing][0] + (8 * (p & 1) + i) * kPcKPitch;
+      const uint64_t rowaddr = row_tab[rec];
+      const bool valid = !(rowaddr & 1u);
+      if (kPacked) {
+        // a record staged from an odd pool row starts 8 bytes in: read the
+        // bitmap word and scales at both offsets in one round trip
+        const u32x4 wpair = {*(const uint32_t*)(st + kCodeBytes + 8 * wd),
+                             *(const uint32_t*)(st + kCodeBytes + 8 * wd + 4),
+                             *(const uint32_t*)(st + kCodeBytes + 8 * wd + 8),
+                             *(const uint32_t*)(st + kCodeBytes + 8 * wd + 12)};
+        const uint32_t sc0 = *(const uint32_t*)(st + kDataBytes + 4 * (wd >> 2));
+        const uint32_t sc1 = *(const uint32_t*)(st + kDataBytes + 8 + 4 * (wd >> 2));
+        const bool odd = (rowaddr & 8u) != 0;
+        const uint32_t wlo = valid ? (odd ? wpair[2] : wpair[0]) : 0u;
+        const uint32_t whi = valid ? (odd ? wpair[3] : wpair[1]) : 0u;
+        const uint64_t word = ((uint64_t)whi << 32) | wlo;
+        const uint32_t sw = valid ? (odd ? sc1 : sc0) : 0u;
+        const float scale = exp2i((int)((sw >> (8 * (wd & 3))) & 0xffu) - 127);
+        // codes before this word: exclusive prefix over the record's lanes
+        // i + 8 w. A 16-lane row holds words 2k, 2k + 1: pair sums in the row
+        // (DPP), row totals combined across rows with the permlane swaps.
+        const int cnt = __popcll(word);
+        const int y = cnt + __builtin_amdgcn_update_dpp(0, cnt, 0x118, 0xf, 0xf, true);  // row_shr:8
+        const int t8 = __builtin_amdgcn_update_dpp(0, y, 0x108, 0xf, 0xf, true);         // row_shl:8
+        const int tot = (wd & 1) ? y : t8;  // words 2k + 2k+1, in every lane of row k
+        const auto h = __builtin_amdgcn_permlane16_swap((uint32_t)tot, (uint32_t)tot, false, false);
+        const int other = (wd & 2) ? (int)h[0] : (int)h[1];  // total of the paired row
+        int before = (wd & 2) ? other : 0;
+        const int pair = tot + other;  // rows 0+1 or 2+3
+        const auto q = __builtin_amdgcn_permlane32_swap((uint32_t)pair, (uint32_t)pair, false, false);
+        before += (wd & 4) ? (int)q[0] : 0;
+        // LDS byte address of the next code: the staged record (4-byte aligned)
+        // plus the codes before it; its low two bits align the code window
+        uint32_t r = lds_addr(st) + (odd ? 8u : 0u) + (uint32_t)(before + y - cnt);
+        uint32_t d0[8], d1[8], d2[8], rk[8];
+        uint64_t sel[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const uint32_t byte = c < 4 ? (whi >> (24 - 8 * c)) & 0xffu : (wlo >> (56 - 8 * c)) & 0xffu;
+          const lds_u32* cw = (const lds_u32*)(uintptr_t)(r & ~3u);
+          d0[c] = cw[0];
+          d1[c] = cw[1];
+          d2[c] = cw[2];
+          sel[c] = sel_tab[byte];
+          rk[c] = r;
+          r += __popc(byte);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const uint32_t lo4 = __builtin_amdgcn_alignbyte(d1[c], d0[c], rk[c]);
+          const uint32_t hi4 = __builtin_amdgcn_alignbyte(d2[c], d1[c], rk[c]);
+          const uint32_t lo = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)sel[c]);
+          const uint32_t hi = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)(sel[c] >> 32));
+          *(u32x4*)(krow + 64 * wd + 8 * c) =
+              u32x4{cvt2<false>(lo, scale), cvt2<true>(lo, scale), cvt2<false>(hi, scale),
+                    cvt2<true>(hi, scale)};
+        }
+        if (a.freqs) {
+          // tail: lane (i, j) rotates pairs 4j..4j+3 of record i (BF16 in, BF16 out)
+          wave_lds_sync();
+          uint16_t* tail = krow + kNopeDim + 8 * wd;
+          const u32x4 v = *(const u32x4*)tail;
+          const uint8_t* fb = &raw[p][B][0] + G::kFreqAt + 16 * i;
+          // (an invalid record's tail is zero and its stand-in RoPE row finite)
+          const f32x4 f0 = *(const f32x4*)(fb + 256 * wd);        // piece 2j
+          const f32x4 f1 = *(const f32x4*)(fb + 256 * wd + 128);  // piece 2j + 1
+          float x8[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x8[2 * e] = u2f(v[e] << 16);
+            x8[2 * e + 1] = u2f(v[e] & 0xffff0000u);
+          }
+          float cs[8] = {f0[0], f0[1], f0[2], f0[3], f1[0], f1[1], f1[2], f1[3]};
+          rope4(x8, cs);
+          const bf16x8 rot = {(__bf16)x8[0], (__bf16)x8[1], (__bf16)x8[2], (__bf16)x8[3],
+                              (__bf16)x8[4], (__bf16)x8[5], (__bf16)x8[6], (__bf16)x8[7]};
+          *(bf16x8*)tail = rot;
+        }
+      } else {
+        const uint32_t sw0 = *(const uint32_t*)(&raw[p][B][0] + G::kScaleAt + 8 * i + 4 * (wd >> 2));
+        u32x4 in0[4], in1[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {  // Nope word: 16 codes per piece; tail: 8 BF16 x 2
+          const uint8_t* src = wd < 7 ? st + 64 * wd + 16 * c : st + kNopeDim + 32 * c;
+          in0[c] = *(const u32x4*)src;
+          in1[c] = *(const u32x4*)(src + 16);
+        }
+        const uint32_t sw = valid ? sw0 : 0u;
+        const float scale = exp2i((int)((sw >> (8 * (wd & 3))) & 0xffu) - 127);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          u32x4 out0, out1;
+          if (wd < 7) {  // 16 E4M3 codes -> two 8-coordinate chunks
+            const u32x4 codes = valid ? in0[c] : u32x4{0u, 0u, 0u, 0u};
+            out0 = u32x4{cvt2<false>(codes[0], scale), cvt2<true>(codes[0], scale),
+                         cvt2<false>(codes[1], scale), cvt2<true>(codes[1], scale)};
+            out1 = u32x4{cvt2<false>(codes[2], scale), cvt2<true>(codes[2], scale),
+                         cvt2<false>(codes[3], scale), cvt2<true>(codes[3], scale)};
+          } else {  // tail: rotated BF16 as stored
+            out0 = valid ? in0[c] : u32x4{0u, 0u, 0u, 0u};
+            out1 = valid ? in1[c] : u32x4{0u, 0u, 0u, 0u};
+          }
+          *(u32x4*)(krow + 64 * wd + 16 * c) = out0;
+          *(u32x4*)(krow + 64 * wd + 16 * c + 8) = out1;
+        }
+      }
+    };
+
+    // One stage step in ring phase B (the stage loop is unrolled by D so the
+    // RoPE registers of each ring buffer are fixed).
+    auto step = [&](int s, auto bufc) {
+      constexpr int B = decltype(bufc)::value;
+      // this wave's loads for stage s are done once at most the later D - 2
+      // stages' loads remain outstanding
+      wait_vm_upto<(D - 2) * G::kLoads>();
+      wave_lds_sync();
+      block_sync_lds();  // ring slots of stage s free (consumers are on stage s - 1)
+      issue_stage(s + D - 1, std::integral_constant<int, (B + D - 1) % D>{});  // past the end: fillers
+      if (s < stages) produce(s, bufc);
+    };
+
+    for (int pass = 0; pass < 2; ++pass) {
+      issue_stage(0, std::integral_constant<int, 0>{});
+      issue_stage(1, std::integral_constant<int, 1>{});
+      if (D > 3) issue_stage(2, std::integral_constant<int, 2 % D>{});
+      for (int s0 = 0; s0 <= stages; s0 += D) {
+        step(s0, std::integral_constant<int, 0>{});
+        if (s0 + 1 <= stages) step(s0 + 1, std::integral_constant<int, 1>{});
+        if (s0 + 2 <= stages) step(s0 + 2, std::integral_constant<int, 2>{});
+        if (D > 3 && s0 + 3 <= stages) step(s0 + 3, std::integral_constant<int, 3 % D>{});
+      }
+      wait_vm();  // drain the filler copies
+      __syncthreads();  // consumers' maxima published
+      float mtrue;
+      const bool redo = redo_pass(mtrue);
+      __syncthreads();
+      if (!redo) break;
+    }
+    return;
+  }
+
+  // ================= consumer =================
+  // Consumer c owns output coordinates 256 c .. 256 c + 255 of the 16 heads.
+  // Both consumers score every tile, so their softmax state (reference, sum)
+  // is identical and each finalises its half of O on its own.
+  const int g = lane >> 4, col = lane & 15;
+  const int half = wv;  // 0 or 1
+  f32x4 o[16];          // O[head 4g + i][256 half + 16 nt + col]
+  float m_ref = -INFINITY, m_seen = -INFINITY, l_run = 0.0f;
+
+  // One stage: tiles 2s' and 2s' + 1 of the ring (slots sa, sb; records
+  // tile0 .. tile0 + 31). S^T for each tile on v_mfma_f32_16x16x32_bf16, then
+  // O[:, half] += P K over the 32 records on v_mfma_f32_16x16x32_bf16: lane
+  // (g, col) holds P[head col][records 4g .. 4g+3 of both tiles] -- exactly the
+  // A operand with k = 8 g + j <-> (tile j / 4, record 4 g + j % 4) -- and the
+  // B operand is the two transposed K reads of the same records. Branch-free,
+  // so the scheduling groups at the end can pipeline the LDS reads.
+  auto consume = [&](int sa, int sb, int tile0) {
+    const uint16_t* kta = &ktile[sa][0];
+    const uint16_t* ktb = &ktile[sb][0];
+    const uint64_t ra = row_tab[tile0 + col], rb = row_tab[tile0 + kT + col];
+    const uint64_t va = __ballot(lane < kT && !(ra & 1u));
+    const uint64_t vb = __ballot(lane < kT && !(rb & 1u));
+    const uint16_t* kra = kta + col * kPcKPitch + 8 * g;
+    const uint16_t* krb = ktb + col * kPcKPitch + 8 * g;
+    f32x4 sa4 = {0.f, 0.f, 0.f, 0.f}, sb4 = sa4;  // lane: S^T[rec 4g + i][head col]
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {  // two independent accumulation chains
+      sa4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          __builtin_bit_cast(bf16x8, *(const u32x4*)(kra + 32 * ks)), qf[ks], sa4, 0, 0, 0);
+      sb4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          __builtin_bit_cast(bf16x8, *(const u32x4*)(krb + 32 * ks)), qf[ks], sb4, 0, 0, 0);
+    }
+    float sv[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sv[i] = ((va >> (4 * g + i)) & 1u) ? sa4[i] * a.scale_log2 : -INFINITY;
+      sv[4 + i] = ((vb >> (4 * g + i)) & 1u) ? sb4[i] * a.scale_log2 : -INFINITY;
+    }
+    float mt = sv[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mt = fmaxf(mt, sv[i]);
+    m_seen = fmaxf(m_seen, mt);
+    // reference: the first stage with a valid record sets it for every head
+    mt = max_over_rows(mt);
+    m_ref = m_ref == -INFINITY ? mt : m_ref;
+    const float mr = m_ref == -INFINITY ? 0.0f : m_ref;
+    float pr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pr[i] = __builtin_amdgcn_exp2f(sv[i] - mr);
+      l_run += pr[i];
+    }
+    const bf16x8 pa = {(__bf16)pr[0], (__bf16)pr[1], (__bf16)pr[2], (__bf16)pr[3],
+                       (__bf16)pr[4], (__bf16)pr[5], (__bf16)pr[6], (__bf16)pr[7]};
+    const int vo = (4 * g + (col >> 2)) * kPcKPitch + 4 * (col & 3) + 256 * half;
+#pragma unroll
+    for (int nt = 0; nt < 16; ++nt) {
+      const s16x4 ka = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(kta + vo + 16 * nt));
+      const s16x4 kb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(ktb + vo + 16 * nt));
+      const s16x8 kab = {ka[0], ka[1], ka[2], ka[3], kb[0], kb[1], kb[2], kb[3]};
+      o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, __builtin_bit_cast(bf16x8, kab), o[nt],
+                                                      0, 0, 0);
+    }
+    // S: K reads run 8 ahead of the MFMAs; the first 8 PV reads overlap the
+    // last S MFMAs and the softmax; PV reads then run 8 ahead.
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+#pragma unroll
+    for (int k = 0; k < 24; ++k) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+  };
+
+  // Pass 0 takes the reference from the first valid stage; a split whose
+  // scores exceed it by more than 2^kRefSlack is recomputed once against its
+  // true max.
+  for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+    for (int nt = 0; nt < 16; ++nt) o[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    l_run = 0.0f;
+    for (int s = 0; s <= stages; ++s) {
+      block_sync_lds();  // stage s - 1 in the ring
+      if (s >= 1) consume((2 * s - 2) % kPcRing, (2 * s - 1) % kPcRing, (s - 1) * kPcStage);
+    }
+    m_seen = fmaxf(m_seen, __shfl_xor(m_seen, 16, 64));
+    m_seen = fmaxf(m_seen, __shfl_xor(m_seen, 32, 64));
+    if (lane < 16) {
+      mrg[wv][0][lane] = m_ref;
+      mrg[wv][1][lane] = m_seen;
+    }
+    __syncthreads();
+    float mtrue;
+    const bool redo = redo_pass(mtrue);
+    __syncthreads();
+    if (!redo) break;
+    m_ref = __shfl(mtrue, col, 64);  // reference: the true max
+  }
+
+  // ---- finalise this consumer's half of O ----
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);  // sum of the weights of head col against m_ref
+  const float mm = m_ref;
+  float factor_h, lse_h;
+  if (a.splits == 1) {
+    const float sink2 = a.sink ? a.sink[head0 + col] * kLog2e : -INFINITY;
+    const float mz = fmaxf(mm, sink2);
+    factor_h = 0.0f;
+    lse_h = -INFINITY;
+    if (mz != -INFINITY) {
+      const float em = mm == -INFINITY ? 0.0f : exp2f(mm - mz);
+      const float z = l_run * em + exp2f(sink2 - mz);
+      factor_h = em / z;
+      lse_h = (mz + log2f(z)) * kLn2;
+    }
+    if (half == 0 && lane < 16) a.lse[t * a.heads + head0 + col] = lse_h;
+  } else {
+    factor_h = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    lse_h = l_run > 0.0f ? mm + log2f(l_run) : -INFINITY;
+    if (half == 0 && lane < 16) a.ws_lse[(t * a.splits + split) * a.heads + head0 + col] = lse_h;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * g + i;
+    const float f = __shfl(factor_h, h, 64);
+    if (a.splits == 1) {
+      uint16_t* orow = a.out + (t * a.heads + head0 + h) * kHeadDim + 256 * half + col;
+#pragma unroll
+      for (int nt = 0; nt < 16; ++nt)
+        orow[16 * nt] = __builtin_bit_cast(uint16_t, (__bf16)(o[nt][i] * f));
+    } else {
+      float* orow = a.ws_o + ((t * a.splits + split) * a.heads + head0 + h) * kHeadDim +
+                    256 * half + col;
+#pragma unroll
+      for (int nt = 0; nt < 16; ++nt) orow[16 * nt] = o[nt][i] * f;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kPcThreads) void packed_decode_pc_kernel(DecodeArgs a) {
+  decode_pc<true>(a);
+}
+__global__ __launch_bounds__(kPcThreads) void native_decode_pc_kernel(DecodeArgs a) {
+  decode_pc<false>(a);
+}
+
 // Merge split partials with the sink. One workgroup (4 waves) per (token,
 // head) row: wave w takes splits w, w+4, ...; lane l owns coordinates
 // 8l..8l+7; the 4 partial sums meet in LDS in a fixed order.
@@ -629,6 +1122,28 @@ Plan plan_for(int64_t tokens, int64_t heads, int64_t topk) {
   return p;
 }
 
+// Producer/consumer plan: about one workgroup per CU (256), whole 32-record
+// stages per split, at most kPcMaxChunk records per split.
+Plan plan_pc(int64_t tokens, int64_t heads, int64_t topk) {
+  const int64_t base = tokens * (heads / 16);
+  const int64_t stages = (topk + kPcStage - 1) / kPcStage;
+  int64_t splits = base > 0 ? (256 + base - 1) / base : 1;
+  const int64_t min_splits = (topk + kPcMaxChunk - 1) / kPcMaxChunk;
+  if (splits > stages) splits = stages;
+  if (splits > kMaxSplits) splits = kMaxSplits;
+  if (splits < min_splits) splits = min_splits;
+  if (splits < 1) splits = 1;
+  int64_t chunk_stages = (stages + splits - 1) / splits;
+  if (chunk_stages < 1) chunk_stages = 1;
+  splits = (stages + chunk_stages - 1) / chunk_stages;
+  if (splits < 1) splits = 1;
+  Plan p;
+  p.splits = (int)splits;
+  p.chunk = (int)(chunk_stages * kPcStage);
+  p.bytes = splits > 1 ? (size_t)(tokens * splits * heads) * (kHeadDim + 1) * sizeof(float) : 0;
+  return p;
+}
+
 bool aligned(const void* p, uintptr_t al) { return ((uintptr_t)p & (al - 1)) == 0; }
 
 template <bool kPacked>
@@ -652,7 +1167,7 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
       (freqs && !aligned(freqs, 16)))
     return RM_ERR_ALIGN;
   if (tokens > 65535) return RM_ERR_SHAPE;
-  const Plan plan = plan_for(tokens, heads, topk);
+  const Plan plan = plan_pc(tokens, heads, topk);
   if (plan.bytes > 0 && (!workspace || workspace_bytes < plan.bytes)) return RM_ERR_WORKSPACE;
   if (plan.bytes > 0 && !aligned(workspace, 16)) return RM_ERR_ALIGN;
   DecodeArgs a;
@@ -680,9 +1195,9 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   a.ws_lse = plan.bytes ? (float*)workspace + (size_t)tokens * plan.splits * heads * kHeadDim
                         : nullptr;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(kPacked ? packed_decode_kernel : native_decode_kernel,
+  hipLaunchKernelGGL(kPacked ? packed_decode_pc_kernel : native_decode_pc_kernel,
                      dim3((unsigned)plan.splits, (unsigned)tokens, (unsigned)(heads / 16)),
-                     dim3(kThreads), 0, s, a);
+                     dim3(kPcThreads), 0, s, a);
   if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   if (plan.splits > 1) {
     const int64_t rows = tokens * heads;
@@ -700,7 +1215,7 @@ extern "C" int rm_sparse_decode_workspace(int64_t tokens, int64_t heads, int64_t
   if (tokens < 0 || heads < 0 || heads % 16 || topk < 0 ||
       topk > (int64_t)kMaxChunk * kMaxSplits)
     return RM_ERR_SHAPE;
-  const Plan p = plan_for(tokens, heads, topk);
+  const Plan p = plan_pc(tokens, heads, topk);
   if (num_splits) *num_splits = p.splits;
   if (workspace_bytes) *workspace_bytes = p.bytes;
   return RM_OK;

@@ -87,7 +87,7 @@ def test_capi_rejects_bad_arguments_without_launching():
     assert lib.rm_sparse_decode_workspace(1, 16, 15361, ctypes.byref(splits),
                                           ctypes.byref(nbytes)) == -2
     assert lib.rm_sparse_decode_workspace(1, 16, 15360, ctypes.byref(splits),
-                                          ctypes.byref(nbytes)) == 0 and splits.value == 64
+                                          ctypes.byref(nbytes)) == 0 and 1 <= splits.value <= 64
 
 
 def test_decode_split_plan():
