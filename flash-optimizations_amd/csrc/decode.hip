@@ -563,6 +563,13 @@ constexpr int kPcThreads = 64 * (kPcConsumers + kPcProducers);
 constexpr int kPcStage = 32;               // records per stage: two 16-record tiles
 constexpr int kPcRing = 4;                 // K tile slots (two stages)
 constexpr int kPcKPitch = kHeadDim + 16;   // BF16 per K row (1056 B: rows 8 banks apart)
+// Within a K row, 8-coordinate chunk q sits at BF16 offset kchunk(q): even
+// chunks in order from 0, odd chunks in order from kPcOddAt (4 banks past the
+// matching even chunk). One pass of the expansion writes 32 even (or odd)
+// chunks of a record contiguously, and the transposed reads of a 16-coordinate
+// group (one even, one odd chunk, 4 rows) cover 32 distinct banks.
+constexpr int kPcOddAt = 264;
+__device__ __forceinline__ constexpr int kchunk(int q) { return (q >> 1) * 8 + (q & 1) * kPcOddAt; }
 constexpr int kPcMaxChunk = 512;           // records per split
 // instruction classes of __builtin_amdgcn_sched_group_barrier
 constexpr int kSchedMfma = 0x008;
@@ -582,7 +589,7 @@ struct PcGeo {
   static constexpr int kScaleAt = 1024 * kCopies;                      // Native: scale rows
   static constexpr int kBuf = kScaleAt + (kPacked ? 0 : 256);          // bytes per stage buffer
   static constexpr int kLoads = kCopies + (kPacked ? 0 : 1);           // global loads per stage
-  static constexpr int kDepth = 4;                                     // copy ring buffers
+  static constexpr int kDepth = 4;  // copy ring buffers (the step loop is unrolled by 4)
 };
 
 // Max of x over lanes col, col + 16, col + 32, col + 48 (col = lane % 16).
@@ -684,6 +691,7 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a) {
   if (wv >= kPcConsumers) {
     // ================= producer =================
     constexpr int D = G::kDepth;
+    static_assert(D == 4, "the stage loop below is unrolled for a four-buffer ring");
     const int p = wv - kPcConsumers;
     const uint8_t* const dummy = (const uint8_t*)a.q;
     // Copies of stage s into ring buffer B: the record table entries first,
@@ -726,145 +734,181 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a) {
       }
     };
 
-    // Expand this wave's 8 records of stage s (ring buffer B) into the K ring.
-    // Lane (record i = lane % 8, word w = lane / 8) writes the 64 coordinates
-    // of bitmap word w; the eight records of one word sit 8 banks apart.
-    auto produce = [&](int s, auto bufc) {
+    // ---- Packed expansion ----
+    // Lane (record i = lane % 8, word w = lane / 8) expands the 64 coordinates
+    // of bitmap word w of record i: first reads (head), code windows and
+    // selectors (gather), conversion into the K ring (expand), tail rotation.
+    struct Head {  // first reads: record slot, bitmap word and scales at both offsets
+      uint64_t row;
+      uint32_t w[4], sc0, sc1;
+    };
+    struct Gath {  // code windows and selectors of the 8 chunks of this lane's word
+      uint32_t d0[8], d1[8], d2[8], rk[8];
+      uint64_t sel[8];
+      float scale;
+    };
+    const int pi = lane & 7, pw = lane >> 3;
+    auto head = [&](int s, auto bufc, Head& h) {
       constexpr int B = decltype(bufc)::value;
-      const int i = lane & 7, wd = lane >> 3;
-      const int rec = s * kPcStage + 8 * p + i;
-      const uint8_t* st = &raw[p][B][0] + i * G::kPitch;
+      const uint8_t* st = &raw[p][B][0] + pi * G::kPitch;
+      h.row = row_tab[s * kPcStage + 8 * p + pi];
+      // a record staged from an odd pool row starts 8 bytes in
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h.w[e] = *(const uint32_t*)(st + kCodeBytes + 8 * pw + 4 * e);
+      h.sc0 = *(const uint32_t*)(st + kDataBytes + 4 * (pw >> 2));
+      h.sc1 = *(const uint32_t*)(st + kDataBytes + 8 + 4 * (pw >> 2));
+    };
+    auto gather = [&](auto bufc, const Head& h, Gath& gt) {
+      constexpr int B = decltype(bufc)::value;
+      const uint8_t* st = &raw[p][B][0] + pi * G::kPitch;
+      const bool valid = !(h.row & 1u), odd = (h.row & 8u) != 0;
+      const uint32_t wlo = valid ? (odd ? h.w[2] : h.w[0]) : 0u;
+      const uint32_t whi = valid ? (odd ? h.w[3] : h.w[1]) : 0u;
+      const uint32_t sw = valid ? (odd ? h.sc1 : h.sc0) : 0u;
+      gt.scale = exp2i((int)((sw >> (8 * (pw & 3))) & 0xffu) - 127);
+      // codes before this word: exclusive prefix over the record's lanes
+      // i + 8 w. A 16-lane row holds words 2k, 2k + 1: pair sums in the row
+      // (DPP), row totals combined across rows with the permlane swaps.
+      const int cnt = __popc(wlo) + __popc(whi);
+      const int y = cnt + __builtin_amdgcn_update_dpp(0, cnt, 0x118, 0xf, 0xf, true);  // row_shr:8
+      const int t8 = __builtin_amdgcn_update_dpp(0, y, 0x108, 0xf, 0xf, true);         // row_shl:8
+      const int tot = (pw & 1) ? y : t8;  // words 2k + 2k+1, in every lane of row k
+      const auto hs = __builtin_amdgcn_permlane16_swap((uint32_t)tot, (uint32_t)tot, false, false);
+      const int other = (pw & 2) ? (int)hs[0] : (int)hs[1];  // total of the paired row
+      int before = (pw & 2) ? other : 0;
+      const int pair = tot + other;  // rows 0+1 or 2+3
+      const auto qs = __builtin_amdgcn_permlane32_swap((uint32_t)pair, (uint32_t)pair, false, false);
+      before += (pw & 4) ? (int)qs[0] : 0;
+      // LDS byte address of the next code: the staged record (4-byte aligned)
+      // plus the codes before it; its low two bits align the code window
+      uint32_t r = lds_addr(st) + (odd ? 8u : 0u) + (uint32_t)(before + y - cnt);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t byte = c < 4 ? (whi >> (24 - 8 * c)) & 0xffu : (wlo >> (56 - 8 * c)) & 0xffu;
+        const lds_u32* cw = (const lds_u32*)(uintptr_t)(r & ~3u);
+        gt.d0[c] = cw[0];
+        gt.d1[c] = cw[1];
+        gt.d2[c] = cw[2];
+        gt.sel[c] = sel_tab[byte];
+        gt.rk[c] = r;
+        r += __popc(byte);
+      }
+    };
+    auto expand = [&](int s, const Gath& gt) {
       uint16_t* const krow =
-          &ktile[(2 * s + (p >> 1)) % kPcRing][0] + (8 * (p & 1) + i) * kPcKPitch;
-      const uint64_t rowaddr = row_tab[rec];
-      const bool valid = !(rowaddr & 1u);
-      if (kPacked) {
-        // a record staged from an odd pool row starts 8 bytes in: read the
-        // bitmap word and scales at both offsets in one round trip
-        const u32x4 wpair = {*(const uint32_t*)(st + kCodeBytes + 8 * wd),
-                             *(const uint32_t*)(st + kCodeBytes + 8 * wd + 4),
-                             *(const uint32_t*)(st + kCodeBytes + 8 * wd + 8),
-                             *(const uint32_t*)(st + kCodeBytes + 8 * wd + 12)};
-        const uint32_t sc0 = *(const uint32_t*)(st + kDataBytes + 4 * (wd >> 2));
-        const uint32_t sc1 = *(const uint32_t*)(st + kDataBytes + 8 + 4 * (wd >> 2));
-        const bool odd = (rowaddr & 8u) != 0;
-        const uint32_t wlo = valid ? (odd ? wpair[2] : wpair[0]) : 0u;
-        const uint32_t whi = valid ? (odd ? wpair[3] : wpair[1]) : 0u;
-        const uint64_t word = ((uint64_t)whi << 32) | wlo;
-        const uint32_t sw = valid ? (odd ? sc1 : sc0) : 0u;
-        const float scale = exp2i((int)((sw >> (8 * (wd & 3))) & 0xffu) - 127);
-        // codes before this word: exclusive prefix over the record's lanes
-        // i + 8 w. A 16-lane row holds words 2k, 2k + 1: pair sums in the row
-        // (DPP), row totals combined across rows with the permlane swaps.
-        const int cnt = __popcll(word);
-        const int y = cnt + __builtin_amdgcn_update_dpp(0, cnt, 0x118, 0xf, 0xf, true);  // row_shr:8
-        const int t8 = __builtin_amdgcn_update_dpp(0, y, 0x108, 0xf, 0xf, true);         // row_shl:8
-        const int tot = (wd & 1) ? y : t8;  // words 2k + 2k+1, in every lane of row k
-        const auto h = __builtin_amdgcn_permlane16_swap((uint32_t)tot, (uint32_t)tot, false, false);
-        const int other = (wd & 2) ? (int)h[0] : (int)h[1];  // total of the paired row
-        int before = (wd & 2) ? other : 0;
-        const int pair = tot + other;  // rows 0+1 or 2+3
-        const auto q = __builtin_amdgcn_permlane32_swap((uint32_t)pair, (uint32_t)pair, false, false);
-        before += (wd & 4) ? (int)q[0] : 0;
-        // LDS byte address of the next code: the staged record (4-byte aligned)
-        // plus the codes before it; its low two bits align the code window
-        uint32_t r = lds_addr(st) + (odd ? 8u : 0u) + (uint32_t)(before + y - cnt);
-        uint32_t d0[8], d1[8], d2[8], rk[8];
-        uint64_t sel[8];
+          &ktile[(2 * s + (p >> 1)) % kPcRing][0] + (8 * (p & 1) + pi) * kPcKPitch;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const uint32_t byte = c < 4 ? (whi >> (24 - 8 * c)) & 0xffu : (wlo >> (56 - 8 * c)) & 0xffu;
-          const lds_u32* cw = (const lds_u32*)(uintptr_t)(r & ~3u);
-          d0[c] = cw[0];
-          d1[c] = cw[1];
-          d2[c] = cw[2];
-          sel[c] = sel_tab[byte];
-          rk[c] = r;
-          r += __popc(byte);
-        }
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t lo4 = __builtin_amdgcn_alignbyte(gt.d1[c], gt.d0[c], gt.rk[c]);
+        const uint32_t hi4 = __builtin_amdgcn_alignbyte(gt.d2[c], gt.d1[c], gt.rk[c]);
+        const uint32_t lo = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)gt.sel[c]);
+        const uint32_t hi = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)(gt.sel[c] >> 32));
+        *(u32x4*)(krow + kchunk(8 * pw + c)) =
+            u32x4{cvt2<false>(lo, gt.scale), cvt2<true>(lo, gt.scale), cvt2<false>(hi, gt.scale),
+                  cvt2<true>(hi, gt.scale)};
+      }
+    };
+    // tail: lane (i, j) rotates pairs 4j..4j+3 of record i (BF16 in, BF16 out);
+    // an invalid record's tail is zero and its stand-in RoPE row finite; without
+    // a table the rotation is the identity
+    auto rotate = [&](int s, auto bufc) {
+      constexpr int B = decltype(bufc)::value;
+      wave_lds_sync();
+      uint16_t* const tail = &ktile[(2 * s + (p >> 1)) % kPcRing][0] +
+                             (8 * (p & 1) + pi) * kPcKPitch + kchunk(kNopeDim / 8 + pw);
+      const u32x4 v = *(const u32x4*)tail;
+      const uint8_t* fb = &raw[p][B][0] + G::kFreqAt + 16 * pi;
+      const f32x4 f0 = *(const f32x4*)(fb + 256 * pw);        // piece 2j
+      const f32x4 f1 = *(const f32x4*)(fb + 256 * pw + 128);  // piece 2j + 1
+      float x8[8];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const uint32_t lo4 = __builtin_amdgcn_alignbyte(d1[c], d0[c], rk[c]);
-          const uint32_t hi4 = __builtin_amdgcn_alignbyte(d2[c], d1[c], rk[c]);
-          const uint32_t lo = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)sel[c]);
-          const uint32_t hi = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)(sel[c] >> 32));
-          *(u32x4*)(krow + 64 * wd + 8 * c) =
-              u32x4{cvt2<false>(lo, scale), cvt2<true>(lo, scale), cvt2<false>(hi, scale),
-                    cvt2<true>(hi, scale)};
-        }
-        if (a.freqs) {
-          // tail: lane (i, j) rotates pairs 4j..4j+3 of record i (BF16 in, BF16 out)
-          wave_lds_sync();
-          uint16_t* tail = krow + kNopeDim + 8 * wd;
-          const u32x4 v = *(const u32x4*)tail;
-          const uint8_t* fb = &raw[p][B][0] + G::kFreqAt + 16 * i;
-          // (an invalid record's tail is zero and its stand-in RoPE row finite)
-          const f32x4 f0 = *(const f32x4*)(fb + 256 * wd);        // piece 2j
-          const f32x4 f1 = *(const f32x4*)(fb + 256 * wd + 128);  // piece 2j + 1
-          float x8[8];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            x8[2 * e] = u2f(v[e] << 16);
-            x8[2 * e + 1] = u2f(v[e] & 0xffff0000u);
-          }
-          float cs[8] = {f0[0], f0[1], f0[2], f0[3], f1[0], f1[1], f1[2], f1[3]};
-          rope4(x8, cs);
-          const bf16x8 rot = {(__bf16)x8[0], (__bf16)x8[1], (__bf16)x8[2], (__bf16)x8[3],
-                              (__bf16)x8[4], (__bf16)x8[5], (__bf16)x8[6], (__bf16)x8[7]};
-          *(bf16x8*)tail = rot;
-        }
-      } else {
-        const uint32_t sw0 = *(const uint32_t*)(&raw[p][B][0] + G::kScaleAt + 8 * i + 4 * (wd >> 2));
+      for (int e = 0; e < 4; ++e) {
+        x8[2 * e] = u2f(v[e] << 16);
+        x8[2 * e + 1] = u2f(v[e] & 0xffff0000u);
+      }
+      const bool rope = a.freqs != nullptr;
+      float cs[8] = {rope ? f0[0] : 1.f, rope ? f0[1] : 0.f, rope ? f0[2] : 1.f, rope ? f0[3] : 0.f,
+                     rope ? f1[0] : 1.f, rope ? f1[1] : 0.f, rope ? f1[2] : 1.f, rope ? f1[3] : 0.f};
+      rope4(x8, cs);
+      const bf16x8 rot = {(__bf16)x8[0], (__bf16)x8[1], (__bf16)x8[2], (__bf16)x8[3],
+                          (__bf16)x8[4], (__bf16)x8[5], (__bf16)x8[6], (__bf16)x8[7]};
+      *(bf16x8*)tail = rot;
+    };
+
+    // ---- Native expansion: stored codes and rotated tail, per stage ----
+    auto produce_native = [&](int s, auto bufc) {
+      constexpr int B = decltype(bufc)::value;
+        // lane (record i, word w) converts the 64 coordinates of word w; piece
+        // pairs in the order (c + w / 2) % 4 keep a record's lanes on distinct banks
+        const int ni = lane >> 3, nw = lane & 7;
+        const bool nvalid = !(row_tab[s * kPcStage + 8 * p + ni] & 1u);
+        const uint8_t* const rb = &raw[p][B][0];
+        const uint8_t* nst = rb + ni * G::kPitch;
+        uint16_t* const nrow =
+            &ktile[(2 * s + (p >> 1)) % kPcRing][0] + (8 * (p & 1) + ni) * kPcKPitch;
+        const uint32_t sw0 = *(const uint32_t*)(rb + G::kScaleAt + 8 * ni + 4 * (nw >> 2));
         u32x4 in0[4], in1[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {  // Nope word: 16 codes per piece; tail: 8 BF16 x 2
-          const uint8_t* src = wd < 7 ? st + 64 * wd + 16 * c : st + kNopeDim + 32 * c;
+          const int cc = (c + (nw >> 1)) & 3;
+          const uint8_t* src = nw < 7 ? nst + 64 * nw + 16 * cc : nst + kNopeDim + 32 * cc;
           in0[c] = *(const u32x4*)src;
           in1[c] = *(const u32x4*)(src + 16);
         }
-        const uint32_t sw = valid ? sw0 : 0u;
-        const float scale = exp2i((int)((sw >> (8 * (wd & 3))) & 0xffu) - 127);
+        const uint32_t sw = nvalid ? sw0 : 0u;
+        const float scale = exp2i((int)((sw >> (8 * (nw & 3))) & 0xffu) - 127);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
+          const int cc = (c + (nw >> 1)) & 3;
           u32x4 out0, out1;
-          if (wd < 7) {  // 16 E4M3 codes -> two 8-coordinate chunks
-            const u32x4 codes = valid ? in0[c] : u32x4{0u, 0u, 0u, 0u};
+          if (nw < 7) {  // 16 E4M3 codes -> two 8-coordinate chunks
+            const u32x4 codes = nvalid ? in0[c] : u32x4{0u, 0u, 0u, 0u};
             out0 = u32x4{cvt2<false>(codes[0], scale), cvt2<true>(codes[0], scale),
                          cvt2<false>(codes[1], scale), cvt2<true>(codes[1], scale)};
             out1 = u32x4{cvt2<false>(codes[2], scale), cvt2<true>(codes[2], scale),
                          cvt2<false>(codes[3], scale), cvt2<true>(codes[3], scale)};
           } else {  // tail: rotated BF16 as stored
-            out0 = valid ? in0[c] : u32x4{0u, 0u, 0u, 0u};
-            out1 = valid ? in1[c] : u32x4{0u, 0u, 0u, 0u};
+            out0 = nvalid ? in0[c] : u32x4{0u, 0u, 0u, 0u};
+            out1 = nvalid ? in1[c] : u32x4{0u, 0u, 0u, 0u};
           }
-          *(u32x4*)(krow + 64 * wd + 16 * c) = out0;
-          *(u32x4*)(krow + 64 * wd + 16 * c + 8) = out1;
+          *(u32x4*)(nrow + kchunk(8 * nw + 2 * cc)) = out0;
+          *(u32x4*)(nrow + kchunk(8 * nw + 2 * cc + 1)) = out1;
         }
-      }
     };
 
     // One stage step in ring phase B (the stage loop is unrolled by D so the
-    // RoPE registers of each ring buffer are fixed).
+    // ring buffer of each step is fixed).
     auto step = [&](int s, auto bufc) {
       constexpr int B = decltype(bufc)::value;
-      // this wave's loads for stage s are done once at most the later D - 2
-      // stages' loads remain outstanding
+      // this wave's loads for stage s are done once at most those of the later
+      // D - 2 stages remain outstanding
       wait_vm_upto<(D - 2) * G::kLoads>();
       wave_lds_sync();
       block_sync_lds();  // ring slots of stage s free (consumers are on stage s - 1)
       issue_stage(s + D - 1, std::integral_constant<int, (B + D - 1) % D>{});  // past the end: fillers
-      if (s < stages) produce(s, bufc);
+      if (s < stages) {
+        if constexpr (kPacked) {
+          Head h;
+          Gath gt;
+          head(s, bufc, h);
+          gather(bufc, h, gt);
+          expand(s, gt);
+          rotate(s, bufc);
+        } else {
+          produce_native(s, bufc);
+        }
+      }
     };
 
     for (int pass = 0; pass < 2; ++pass) {
       issue_stage(0, std::integral_constant<int, 0>{});
       issue_stage(1, std::integral_constant<int, 1>{});
-      if (D > 3) issue_stage(2, std::integral_constant<int, 2 % D>{});
+      issue_stage(2, std::integral_constant<int, 2>{});
       for (int s0 = 0; s0 <= stages; s0 += D) {
         step(s0, std::integral_constant<int, 0>{});
         if (s0 + 1 <= stages) step(s0 + 1, std::integral_constant<int, 1>{});
         if (s0 + 2 <= stages) step(s0 + 2, std::integral_constant<int, 2>{});
-        if (D > 3 && s0 + 3 <= stages) step(s0 + 3, std::integral_constant<int, 3 % D>{});
+        if (s0 + 3 <= stages) step(s0 + 3, std::integral_constant<int, 3>{});
       }
       wait_vm();  // drain the filler copies
       __syncthreads();  // consumers' maxima published
@@ -898,15 +942,16 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a) {
     const uint64_t ra = row_tab[tile0 + col], rb = row_tab[tile0 + kT + col];
     const uint64_t va = __ballot(lane < kT && !(ra & 1u));
     const uint64_t vb = __ballot(lane < kT && !(rb & 1u));
-    const uint16_t* kra = kta + col * kPcKPitch + 8 * g;
-    const uint16_t* krb = ktb + col * kPcKPitch + 8 * g;
+    const int ko = col * kPcKPitch + kchunk(g);  // chunk 4 ks + g at ko + 16 ks
+    const uint16_t* kra = kta + ko;
+    const uint16_t* krb = ktb + ko;
     f32x4 sa4 = {0.f, 0.f, 0.f, 0.f}, sb4 = sa4;  // lane: S^T[rec 4g + i][head col]
 #pragma unroll
     for (int ks = 0; ks < 16; ++ks) {  // two independent accumulation chains
       sa4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          __builtin_bit_cast(bf16x8, *(const u32x4*)(kra + 32 * ks)), qf[ks], sa4, 0, 0, 0);
+          __builtin_bit_cast(bf16x8, *(const u32x4*)(kra + 16 * ks)), qf[ks], sa4, 0, 0, 0);
       sb4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          __builtin_bit_cast(bf16x8, *(const u32x4*)(krb + 32 * ks)), qf[ks], sb4, 0, 0, 0);
+          __builtin_bit_cast(bf16x8, *(const u32x4*)(krb + 16 * ks)), qf[ks], sb4, 0, 0, 0);
     }
     float sv[8];
 #pragma unroll
@@ -930,11 +975,14 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a) {
     }
     const bf16x8 pa = {(__bf16)pr[0], (__bf16)pr[1], (__bf16)pr[2], (__bf16)pr[3],
                        (__bf16)pr[4], (__bf16)pr[5], (__bf16)pr[6], (__bf16)pr[7]};
-    const int vo = (4 * g + (col >> 2)) * kPcKPitch + 4 * (col & 3) + 256 * half;
+    // coordinates 256 half + 16 nt + 4 (col % 4) .. + 3 of record row 4g + col / 4:
+    // chunk 32 half + 2 nt + (col % 4) / 2 at vo + 8 nt
+    const int vo = (4 * g + (col >> 2)) * kPcKPitch + kchunk(((col & 3) >> 1) + 32 * half) +
+                   4 * (col & 1);
 #pragma unroll
     for (int nt = 0; nt < 16; ++nt) {
-      const s16x4 ka = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(kta + vo + 16 * nt));
-      const s16x4 kb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(ktb + vo + 16 * nt));
+      const s16x4 ka = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(kta + vo + 8 * nt));
+      const s16x4 kb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(ktb + vo + 8 * nt));
       const s16x8 kab = {ka[0], ka[1], ka[2], ka[3], kb[0], kb[1], kb[2], kb[3]};
       o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, __builtin_bit_cast(bf16x8, kab), o[nt],
                                                       0, 0, 0);
