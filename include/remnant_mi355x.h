@@ -114,7 +114,7 @@ int rm_sparse_decode_workspace(int64_t tokens, int64_t heads, int64_t topk,
  * record r of request b is pool slot block_table[b, r / 64] * 64 + r % 64.
  * max_blocks: valid columns of the block table. seqlens: [batch] int32 records
  * per request (NULL = unbounded). indices: [batch * q_len, topk] int32 logical
- * records (-1 = padding), topk <= 15360. topk_length: [batch * q_len] int32
+ * records (-1 = padding), topk <= 32768. topk_length: [batch * q_len] int32
  * (NULL = topk).
  * sink: [heads] f32 logits (NULL = no sink). freqs/freq_rows: RoPE table for
  * the stored pre-RoPE tail, row = record * 4 (NULL = tail used as stored).

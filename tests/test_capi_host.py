@@ -81,13 +81,13 @@ def test_capi_rejects_bad_arguments_without_launching():
     assert lib.rm_remnant_sparse_decode_fwd(*args) == -5  # split plan needs a workspace
     assert lib.rm_native_sparse_decode_fwd(x, 0, 1, 16, pool, 1, s, 4, 4, None, s, 8, None,
                                            None, 0.1, x, w, None, 0, None) == 0
-    args[11] = 15361  # top-k beyond 64 splits of 240 records
+    args[11] = 32769  # top-k beyond 64 splits of 512 records
     assert lib.rm_remnant_sparse_decode_fwd(*args) == -2
     splits, nbytes = ctypes.c_int32(), ctypes.c_size_t()
-    assert lib.rm_sparse_decode_workspace(1, 16, 15361, ctypes.byref(splits),
+    assert lib.rm_sparse_decode_workspace(1, 16, 32769, ctypes.byref(splits),
                                           ctypes.byref(nbytes)) == -2
-    assert lib.rm_sparse_decode_workspace(1, 16, 15360, ctypes.byref(splits),
-                                          ctypes.byref(nbytes)) == 0 and 1 <= splits.value <= 64
+    assert lib.rm_sparse_decode_workspace(1, 16, 32768, ctypes.byref(splits),
+                                          ctypes.byref(nbytes)) == 0 and splits.value == 64
 
 
 def test_decode_split_plan():
