@@ -85,10 +85,6 @@ struct DecodeArgs {
   float* ws_lse;   // [tokens, splits, heads]
 };
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return bf16_rne(a) | (bf16_rne(b) << 16);
-}
-
 // Two E4M3 codes (bytes 0-1, or 2-3 with kHi) times scale -> two BF16 (exact).
 template <bool kHi>
 __device__ __forceinline__ uint32_t cvt2(uint32_t codes, float scale) {
@@ -657,10 +653,10 @@ __global__ __launch_bounds__(kPcThreads) void native_decode_pc_kernel(DecodeArgs
   decode_pc<false>(a);
 }
 
-// Merge split partials with the sink. One workgroup (4 waves) per (token,
-// head) row: wave w takes splits w, w+4, ...; lane l owns coordinates
-// 8l..8l+7; the 4 partial sums meet in LDS in a fixed order.
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ ws_o,
+// Merge split partials with the sink, for many rows. One workgroup (4 waves)
+// per (token, head) row: wave w takes splits w, w+4, ...; lane l owns
+// coordinates 8l..8l+7; the 4 partial sums meet in LDS in a fixed order.
+__global__ __launch_bounds__(256) void combine_rows_kernel(const float* __restrict__ ws_o,
                                                       const float* __restrict__ ws_lse,
                                                       const float* __restrict__ sink, int splits,
                                                       int64_t heads, uint16_t* __restrict__ out,
@@ -715,9 +711,67 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
       lse_out = (mz + log2f(zt)) * kLn2;
     }
     *(u32x4*)(out + row * kHeadDim + 8 * lane) =
-        u32x4{pack_bf16x2(r0[0], r0[1]), pack_bf16x2(r0[2], r0[3]), pack_bf16x2(r1[0], r1[1]),
-              pack_bf16x2(r1[2], r1[3])};
+        u32x4{bf16_rne(r0[0]) | (bf16_rne(r0[1]) << 16), bf16_rne(r0[2]) | (bf16_rne(r0[3]) << 16),
+              bf16_rne(r1[0]) | (bf16_rne(r1[1]) << 16), bf16_rne(r1[2]) | (bf16_rne(r1[3]) << 16)};
     if (lane == 0) lse[row] = lse_out;
+  }
+}
+
+// Merge split partials with the sink, for few rows (small batches). One
+// workgroup (4 waves) per (token, head, 64-coordinate slice): lane l owns coordinate 64 slice + l; wave w takes
+// splits w, w + 4, ... (<= 16 each, all loads in flight at once); the four
+// partial sums meet in LDS in a fixed order. The split weights come from every
+// split's LSE, read by every wave (lane s holds split s; splits <= 64).
+constexpr int kCombineSlices = kHeadDim / 64;
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ ws_o,
+                                                      const float* __restrict__ ws_lse,
+                                                      const float* __restrict__ sink, int splits,
+                                                      int64_t heads, uint16_t* __restrict__ out,
+                                                      float* __restrict__ lse) {
+  __shared__ float part[4][64];
+  const int lane = wave_lane();
+  const int wave = uniform((int)(threadIdx.x >> 6));
+  const int64_t row = blockIdx.x / kCombineSlices;
+  const int slice = (int)(blockIdx.x - row * kCombineSlices);
+  const int64_t t = row / heads, h = row - t * heads;
+  const int64_t step = heads * kHeadDim;
+  const float* src = ws_o + (t * splits * heads + h) * kHeadDim + 64 * slice + lane;
+  // issue every load first: this wave's partials and all split LSEs
+  constexpr int kPerWave = kMaxSplits / 4;
+  float x[kPerWave];
+#pragma unroll
+  for (int u = 0; u < kPerWave; ++u) {
+    const int s = wave + 4 * u;
+    x[u] = s < splits ? src[s * step] : 0.0f;
+  }
+  const float ls = lane < splits ? ws_lse[(t * splits + lane) * heads + h] : -INFINITY;
+  const float sink2 = sink ? sink[h] * kLog2e : -INFINITY;
+  float mz = fmaxf(ls, sink2);
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) mz = fmaxf(mz, __shfl_xor(mz, d, 64));
+  const float w = (mz != -INFINITY && lane < splits) ? exp2f(ls - mz) : 0.0f;
+  float z = w;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) z += __shfl_xor(z, d, 64);
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kPerWave; ++u) {
+    const int s = wave + 4 * u;
+    const float wu = __shfl(w, s < splits ? s : 0, 64);
+    acc += (s < splits ? wu : 0.0f) * x[u];
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    float lse_out = -INFINITY, r = 0.0f;
+    if (mz != -INFINITY) {
+      const float zt = z + exp2f(sink2 - mz);
+      const float inv = 1.0f / zt;
+      r = (part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane]) * inv;
+      lse_out = (mz + log2f(zt)) * kLn2;
+    }
+    out[row * kHeadDim + 64 * slice + lane] = (uint16_t)bf16_rne(r);
+    if (lane == 0 && slice == 0) lse[row] = lse_out;
   }
 }
 
@@ -806,8 +860,12 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   if (plan.splits > 1) {
     const int64_t rows = tokens * heads;
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)rows), dim3(256), 0, s, a.ws_o, a.ws_lse,
-                       sink, plan.splits, heads, out, lse);
+    if (rows < 256)  // too few rows to fill the GPU: one workgroup per 64 coordinates
+      hipLaunchKernelGGL(combine_kernel, dim3((unsigned)(rows * kCombineSlices)), dim3(256), 0, s,
+                         a.ws_o, a.ws_lse, sink, plan.splits, heads, out, lse);
+    else
+      hipLaunchKernelGGL(combine_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, a.ws_o,
+                         a.ws_lse, sink, plan.splits, heads, out, lse);
     if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   }
   return RM_OK;
