@@ -169,12 +169,25 @@ __global__ __launch_bounds__(256) void unpack_gather_kernel(
       rr[j] = r;
       valid[j] = v;
     }
-    // the whole 328-byte record in one load: lane i reads bytes 8i..8i+7
+    // the whole 328-byte record in one load: lane i reads bytes 8i..8i+7; the
+    // tail lanes' frequency values are loaded in the same round trip
     u32x2 piece[kRows];
 #pragma unroll
     for (int j = 0; j < kRows; ++j) {
       piece[j] = u32x2{0u, 0u};
       if (valid[j] && lane < kRecordBytes / 8) piece[j] = *(const u32x2*)(rec[j] + 8 * lane);
+    }
+    f32x4 fa[kRows], fb[kRows];
+    const bool tail = freqs && lane >= kNopeDim / 8;
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) {
+      fa[j] = f32x4{1.f, 0.f, 1.f, 0.f};
+      fb[j] = f32x4{1.f, 0.f, 1.f, 0.f};
+      if (tail && valid[j]) {
+        const float* f = freqs + (rr[j] * 4) * (2 * kRopePairs) + 8 * (lane - kNopeDim / 8);
+        fa[j] = *(const f32x4*)f;
+        fb[j] = *(const f32x4*)(f + 4);
+      }
     }
     u32x4 o[kRows];
 #pragma unroll
@@ -182,13 +195,12 @@ __global__ __launch_bounds__(256) void unpack_gather_kernel(
       o[j] = dequant_lane(piece[j], lane, sel);
       if (!valid[j]) o[j] = u32x4{0u, 0u, 0u, 0u};
     }
-    if (freqs && lane >= kNopeDim / 8) {
+    if (tail) {
 #pragma unroll
       for (int j = 0; j < kRows; ++j) {
         if (!valid[j]) continue;
         // rotate the BF16 (re, im) pairs with the record's frequency row
-        const float* f = freqs + (rr[j] * 4) * (2 * kRopePairs) + 8 * (lane - kNopeDim / 8);
-        const f32x4 a = *(const f32x4*)f, b = *(const f32x4*)(f + 4);
+        const f32x4 a = fa[j], b = fb[j];
         float cs[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
         float v[8];
 #pragma unroll
