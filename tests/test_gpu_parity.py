@@ -273,10 +273,35 @@ def test_decode_wide_score_range(packed):
 
 @pytest.mark.parametrize("packed", [True, False], ids=["direct", "native"])
 def test_decode_partial_tiles_and_short_lengths(packed):
-    """Top-k of 100 (a partial three-tile group per split) with per-token
-    lengths 100, 37, 0 and 1: records past each length contribute nothing."""
+    """Top-k of 100 (a partial 32-record stage) with per-token lengths 100,
+    37, 0 and 1: records past each length contribute nothing."""
     banner(f"decode partial tiles packed={packed}")
     c = build_decode_case([500, 300, 800, 64], q_len=1, heads=16, topk=100, seed=16,
                           packed=packed)
     c["lens"][:] = np.array([100, 37, 0, 1], np.int32).reshape(c["lens"].shape)
+    check_decode(c)
+
+
+@pytest.mark.parametrize("packed", [True, False], ids=["direct", "native"])
+def test_decode_batch64_log_uniform_contexts(packed):
+    """The batched case at reduced contexts: 64 requests of 4k-32k tokens,
+    top-k 2048 (several 32-record stages per split, one split per CU share)."""
+    banner(f"decode B=64 packed={packed}")
+    ctx = syn.log_uniform_contexts(64, 4096, 32768, 21)
+    c = build_decode_case(ctx, q_len=1, heads=16, topk=2048, seed=21, packed=packed)
+    check_decode(c)
+
+
+def test_decode_many_splits_uneven_topk():
+    """Top-k 1500 over 8 requests: a split plan with a partial last stage."""
+    banner("decode B=8 topk=1500")
+    ctx = syn.log_uniform_contexts(8, 8192, 40000, 22)
+    c = build_decode_case(ctx, q_len=1, heads=16, topk=1500, seed=22)
+    check_decode(c)
+
+
+def test_decode_maximum_topk():
+    """Top-k 32768, the entry point's limit: 64 splits of 512 records."""
+    banner("decode topk=32768")
+    c = build_decode_case([33000], q_len=1, heads=16, topk=32768, seed=23, sink=False)
     check_decode(c)
