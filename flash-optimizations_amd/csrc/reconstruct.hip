@@ -14,6 +14,11 @@
 // the UE8M0 scale, producing BF16 directly. The lanes owning the RoPE tail
 // (56..63) hold whole (re, im) pairs, so the rotation needs no cross-lane
 // traffic.
+//
+// Survivor profiles other than 256 (64..448 in steps of 64) use the same
+// scheme on (K + 72)-byte records: lanes 0..K/8-1 hold the codes, the next 8
+// the bitmap words and the one after them the scales; the 448-survivor record
+// (520 bytes) needs a 65th piece, which every lane loads from the same address.
 #include "remnant_device.h"
 #include "remnant_mi355x.h"
 
@@ -53,16 +58,21 @@ __device__ __forceinline__ int wave_exclusive_sum(int x) {
   return v - x;
 }
 
-// Per-lane dequantization of a Packed record's coordinates 8l..8l+7 (pre-RoPE)
-// as 8 BF16 values. The record is held across the wave: lane i has bytes
-// 8i..8i+7 (`piece`; lanes 0-31 the codes, 32-39 the bitmap words, 40 the
-// scales), so the lane's bitmap word, code run and scale are register reads
-// from other lanes. `sel` maps a bitmap byte to the v_perm selectors that
-// place its kept codes (the next bytes of the code run) and zeros for pruned
-// slots.
-__device__ __forceinline__ u32x4 dequant_lane(u32x2 piece, int lane, const uint64_t* sel) {
+// Per-lane dequantization of a kK-survivor record's coordinates 8l..8l+7
+// (pre-RoPE) as 8 BF16 values. The record is held across the wave: lane i has
+// bytes 8i..8i+7 (`piece`; for 256 survivors lanes 0-31 the codes, 32-39 the
+// bitmap words, 40 the scales; `extra` holds bytes 512..519 when the record is
+// longer than 512 bytes), so the lane's bitmap word, code run and scale are
+// register reads from other lanes. `sel` maps a bitmap byte to the v_perm
+// selectors that place its kept codes (the next bytes of the code run) and
+// zeros for pruned slots.
+template <int kK>
+__device__ __forceinline__ u32x4 dequant_lane(u32x2 piece, u32x2 extra, int lane,
+                                              const uint64_t* sel) {
+  constexpr int kWordLane = kK / 8, kScaleLane = kK / 8 + 8;
   const int word = lane >> 3, sub = lane & 7;
-  const uint32_t wlo = from_lane(piece[0], 32 + word), whi = from_lane(piece[1], 32 + word);
+  const uint32_t wlo = from_lane(piece[0], kWordLane + word);
+  const uint32_t whi = from_lane(piece[1], kWordLane + word);
   const uint64_t mine = ((uint64_t)whi << 32) | wlo;  // coords 64 word .. 64 word + 63, MSB first
   // codes before the word: popcounts of the earlier words (carried by lane 8w+7)
   int rank = wave_exclusive_sum(sub == 7 ? __popcll(mine) : 0);
@@ -81,10 +91,12 @@ __device__ __forceinline__ u32x4 dequant_lane(u32x2 piece, int lane, const uint6
   const uint64_t s = sel[bits];
   const uint32_t c03 = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)s);
   const uint32_t c47 = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)(s >> 32));
-  // scale bytes: lane 40 (a permute reads the value the source lane offers, so
-  // both halves are read uniformly and selected here)
-  const uint32_t sc_lo = __builtin_amdgcn_readlane(piece[0], 40);
-  const uint32_t sc_hi = __builtin_amdgcn_readlane(piece[1], 40);
+  // scale bytes: lane K/8 + 8 (a permute reads the value the source lane
+  // offers, so both halves are read uniformly and selected here)
+  const uint32_t sc_lo = kScaleLane < 64 ? __builtin_amdgcn_readlane(piece[0], kScaleLane & 63)
+                                         : __builtin_amdgcn_readlane(extra[0], 0);
+  const uint32_t sc_hi = kScaleLane < 64 ? __builtin_amdgcn_readlane(piece[1], kScaleLane & 63)
+                                         : __builtin_amdgcn_readlane(extra[1], 0);
   const uint32_t sc = word < 4 ? sc_lo : sc_hi;
   const float scale = exp2i((int)((sc >> (8 * (word & 3))) & 0xffu) - 127);
   return u32x4{cvt2<false>(c03, scale), cvt2<true>(c03, scale), cvt2<false>(c47, scale),
@@ -117,11 +129,14 @@ __device__ __forceinline__ void split_row(int64_t row, const Index& ix, int64_t&
   }
 }
 
-template <bool kNarrow>
+template <bool kNarrow, int kK>
 __global__ __launch_bounds__(256) void unpack_gather_kernel(
     const uint8_t* __restrict__ pool, int64_t pool_rows, const int32_t* __restrict__ physical,
     const int32_t* __restrict__ raw, const int32_t* __restrict__ lengths, Index ix,
     const float* __restrict__ freqs, int64_t freq_rows, uint16_t* __restrict__ out) {
+  static_assert(kK % 64 == 0 && kK >= 64 && kK <= 448, "survivor profiles are 64..448");
+  constexpr int kBytes = kK + kBitmapBytes + kScaleBytes;  // K + 72
+  constexpr int kPieces = kBytes / 8 < 64 ? kBytes / 8 : 64;
   // selector table: byte bits MSB-first = coordinates 0..7; selector byte i is
   // the rank of coordinate i among the kept ones, or 0x0c (a zero byte)
   __shared__ uint64_t sel[256];
@@ -165,17 +180,19 @@ __global__ __launch_bounds__(256) void unpack_gather_kernel(
       bool v = row < ix.total && k < len && p >= 0 && p < pool_rows;
       if (freqs) v = v && r >= 0 && r * 4 < freq_rows;
       const uint32_t pp = v ? (uint32_t)p : 0u;  // pool rows fit in int32
-      rec[j] = pool + (uint64_t)(pp >> 6) * kPageBytes + (pp & 63u) * kRecordBytes;
+      rec[j] = pool + (uint64_t)(pp >> 6) * (kPageRecords * kBytes) + (pp & 63u) * kBytes;
       rr[j] = r;
       valid[j] = v;
     }
-    // the whole 328-byte record in one load: lane i reads bytes 8i..8i+7; the
-    // tail lanes' frequency values are loaded in the same round trip
-    u32x2 piece[kRows];
+    // the whole record in one load: lane i reads bytes 8i..8i+7; the tail
+    // lanes' frequency values are loaded in the same round trip
+    u32x2 piece[kRows], extra[kRows];
 #pragma unroll
     for (int j = 0; j < kRows; ++j) {
       piece[j] = u32x2{0u, 0u};
-      if (valid[j] && lane < kRecordBytes / 8) piece[j] = *(const u32x2*)(rec[j] + 8 * lane);
+      extra[j] = u32x2{0u, 0u};
+      if (valid[j] && lane < kPieces) piece[j] = *(const u32x2*)(rec[j] + 8 * lane);
+      if (kBytes > 512 && valid[j]) extra[j] = *(const u32x2*)(rec[j] + 512);
     }
     f32x4 fa[kRows], fb[kRows];
     const bool tail = freqs && lane >= kNopeDim / 8;
@@ -192,7 +209,7 @@ __global__ __launch_bounds__(256) void unpack_gather_kernel(
     u32x4 o[kRows];
 #pragma unroll
     for (int j = 0; j < kRows; ++j) {
-      o[j] = dequant_lane(piece[j], lane, sel);
+      o[j] = dequant_lane<kK>(piece[j], extra[j], lane, sel);
       if (!valid[j]) o[j] = u32x4{0u, 0u, 0u, 0u};
     }
     if (tail) {
@@ -222,6 +239,28 @@ __global__ __launch_bounds__(256) void unpack_gather_kernel(
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+struct Launch {
+  const uint8_t* pool;
+  int64_t pool_rows;
+  const int32_t *physical, *raw, *lengths;
+  Index ix;
+  const float* freqs;
+  int64_t freq_rows;
+  uint16_t* out;
+};
+
+template <int kK>
+void launch_unpack(bool narrow, int64_t blocks, const Launch& a, hipStream_t s) {
+  if (narrow)
+    hipLaunchKernelGGL((unpack_gather_kernel<true, kK>), dim3((unsigned)blocks), dim3(256), 0, s,
+                       a.pool, a.pool_rows, a.physical, a.raw, a.lengths, a.ix, a.freqs,
+                       a.freq_rows, a.out);
+  else
+    hipLaunchKernelGGL((unpack_gather_kernel<false, kK>), dim3((unsigned)blocks), dim3(256), 0,
+                       s, a.pool, a.pool_rows, a.physical, a.raw, a.lengths, a.ix, a.freqs,
+                       a.freq_rows, a.out);
+}
+
 }  // namespace
 
 extern "C" int rm_unpack_gather_bf16(const uint8_t* pool, int64_t pool_pages,
@@ -231,7 +270,22 @@ extern "C" int rm_unpack_gather_bf16(const uint8_t* pool, int64_t pool_pages,
                                      const int32_t* lengths, int64_t length_stride,
                                      int64_t n_queries, int64_t selected_k, const float* freqs,
                                      int64_t freq_rows, uint16_t* out, void* stream) {
+  return rm_unpack_gather_bf16_k(pool, pool_pages, RM_KEEP_COUNT, physical, physical_stride_q,
+                                 physical_stride_k, raw, raw_stride_q, raw_stride_k, lengths,
+                                 length_stride, n_queries, selected_k, freqs, freq_rows, out,
+                                 stream);
+}
+
+extern "C" int rm_unpack_gather_bf16_k(const uint8_t* pool, int64_t pool_pages, int keep_count,
+                                       const int32_t* physical, int64_t physical_stride_q,
+                                       int64_t physical_stride_k, const int32_t* raw,
+                                       int64_t raw_stride_q, int64_t raw_stride_k,
+                                       const int32_t* lengths, int64_t length_stride,
+                                       int64_t n_queries, int64_t selected_k,
+                                       const float* freqs, int64_t freq_rows, uint16_t* out,
+                                       void* stream) {
   if (n_queries < 0 || selected_k < 0 || pool_pages < 0 || freq_rows < 0) return RM_ERR_SHAPE;
+  if (keep_count < 64 || keep_count > 448 || keep_count % 64) return RM_ERR_SHAPE;
   const int64_t total = n_queries * selected_k;
   if (total == 0) return RM_OK;
   if (!pool || !physical || !lengths || !out || (freqs && !raw)) return RM_ERR_NULL;
@@ -267,13 +321,16 @@ extern "C" int rm_unpack_gather_bf16(const uint8_t* pool, int64_t pool_pages,
     ix.shift = (uint32_t)(l - 1);
   }
   hipStream_t s = (hipStream_t)stream;
-  if (narrow)
-    hipLaunchKernelGGL(unpack_gather_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, pool,
-                       pool_pages * kPageRecords, physical, raw, lengths, ix, freqs, freq_rows,
-                       out);
-  else
-    hipLaunchKernelGGL(unpack_gather_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s,
-                       pool, pool_pages * kPageRecords, physical, raw, lengths, ix, freqs,
-                       freq_rows, out);
+  const Launch a{pool, pool_pages * kPageRecords, physical, raw, lengths, ix, freqs, freq_rows,
+                 out};
+  switch (keep_count) {
+    case 64: launch_unpack<64>(narrow, blocks, a, s); break;
+    case 128: launch_unpack<128>(narrow, blocks, a, s); break;
+    case 192: launch_unpack<192>(narrow, blocks, a, s); break;
+    case 256: launch_unpack<256>(narrow, blocks, a, s); break;
+    case 320: launch_unpack<320>(narrow, blocks, a, s); break;
+    case 384: launch_unpack<384>(narrow, blocks, a, s); break;
+    default: launch_unpack<448>(narrow, blocks, a, s); break;
+  }
   return hipGetLastError() == hipSuccess ? RM_OK : RM_ERR_LAUNCH;
 }

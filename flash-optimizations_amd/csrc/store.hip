@@ -7,12 +7,14 @@
 // Packed arithmetic (reference: training/losses.py:84-95, evaluate.py:65-91,
 // test_integration.py:1588-1619; producer order in
 // docs/agents/numerical-and-validation.md:22-26):
-//   1. keep the 256 largest |x| (raw magnitudes); ties keep lower coordinates;
+//   1. keep the K largest |x| (raw magnitudes; K = 256 by default, or a
+//      survivor profile 64..448 in steps of 64); ties keep lower coordinates;
 //   2. m = masked x; r = RN(1/RN(sqrt(sum(m^2)/512 + eps))), sum in the fixed
 //      lane-then-pairwise-tree order; n = bf16(RN(RN(m*r)*w));
 //   3. per 64-coordinate group: e = ceil(log2(max(amax|n|, 1e-4)/448)),
 //      scale byte e + 127, code = e4m3_rne(n / 2^e);
-//   4. codes of kept coordinates in ascending order, MSB-first bitmap words.
+//   4. codes of kept coordinates in ascending order, MSB-first bitmap words;
+//      the record is K codes + 64 bitmap bytes + 8 scales (K + 72 bytes).
 #include "remnant_device.h"
 #include "remnant_mi355x.h"
 
@@ -21,7 +23,16 @@ using namespace rm;
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kStageSpill = 336;  // 64 scratch bytes after the staged record
+
+// Geometry of a K-survivor Packed record (K = kKeep gives the 328-byte default).
+template <int kK>
+struct Rec {
+  static constexpr int kBytes = kK + kBitmapBytes + kScaleBytes;  // K + 72
+  static constexpr int kPage = kPageRecords * kBytes;
+  static constexpr int kPieces = kBytes / 8;                        // 8-byte stores
+  static constexpr int kSpill = (kBytes + 15) / 16 * 16;  // 64 scratch bytes after it
+  static_assert(kK % 64 == 0 && kK >= 64 && kK <= 448, "survivor profiles are 64..448");
+};
 
 template <bool kBf16>
 __device__ __forceinline__ void load_row8(const void* x, int64_t row, int64_t stride,
@@ -100,14 +111,14 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
-// Keep mask (bit i = coordinate 8*lane + i) of the 256 largest magnitudes.
-// Bit-serial radix select of the 256th largest key, fully unrolled: every step
+// Keep mask (bit i = coordinate 8*lane + i) of the kK largest magnitudes.
+// Bit-serial radix select of the kK-th largest key, fully unrolled: every step
 // compares the 8 keys of each lane against prefix|bit (one ballot per key slot,
 // popcounts on the scalar unit). `at` is the count at the last accepted step,
-// i.e. #{key >= threshold}; only when it exceeds 256 is there a boundary tie
+// i.e. #{key >= threshold}; only when it exceeds kK is there a boundary tie
 // to admit in coordinate order.
-template <bool kBf16>
-__device__ __forceinline__ uint32_t select_top256(const uint32_t* key) {
+template <bool kBf16, int kK>
+__device__ __forceinline__ uint32_t select_top(const uint32_t* key) {
   constexpr int kLow = kBf16 ? 16 : 0;  // bf16 magnitudes have zero low halves
   uint32_t prefix = 0;
   int at = 512;
@@ -117,21 +128,21 @@ __device__ __forceinline__ uint32_t select_top256(const uint32_t* key) {
     int cnt = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) cnt += popc_ballot(key[i] >= cand);
-    const bool take = cnt >= kKeep;
+    const bool take = cnt >= kK;
     prefix = take ? cand : prefix;
     at = take ? cnt : at;
   }
   uint32_t keep = 0;
-  if (at == kKeep) {
+  if (at == kK) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) keep |= (key[i] >= prefix ? 1u : 0u) << i;
     return keep;
   }
-  // admit the (kKeep - #{key > prefix}) lowest-coordinate ties at the threshold
+  // admit the (kK - #{key > prefix}) lowest-coordinate ties at the threshold
   int gt = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) gt += popc_ballot(key[i] > prefix);
-  const int need = kKeep - gt;
+  const int need = kK - gt;
   int before = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) before += lanes_below(__ballot(key[i] == prefix));
@@ -145,12 +156,13 @@ __device__ __forceinline__ uint32_t select_top256(const uint32_t* key) {
   return keep;
 }
 
-template <bool kBf16>
+template <bool kBf16, int kK>
 __global__ __launch_bounds__(256) void pack_rows_kernel(
     const void* __restrict__ x, int64_t stride, const float* __restrict__ weight, float eps,
     const int32_t* __restrict__ slots, int64_t n, uint8_t* __restrict__ pool,
     int64_t pool_rows) {
-  __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][kStageSpill + 64];
+  using R = Rec<kK>;
+  __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][R::kSpill + 64];
   const int lane = wave_lane();
   const int wave = uniform((int)(threadIdx.x >> 6));
   uint8_t* st = stage[wave];
@@ -172,7 +184,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     load_row8<kBf16>(x, rec, stride, lane, v);
 #pragma unroll
     for (int i = 0; i < 8; ++i) key[i] = f2u(v[i]) & 0x7fffffffu;
-    const uint32_t keep = select_top256<kBf16>(key);
+    const uint32_t keep = select_top<kBf16, kK>(key);
 
     // masked RMSNorm
     float m[8];
@@ -221,7 +233,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     // per-lane spill byte past the record, so the stores are unconditional
     const int cnt = __popc(keep);
     uint8_t* const base = st + wave_exclusive_sum(cnt);
-    uint8_t* const spill = st + kStageSpill + lane;
+    uint8_t* const spill = st + R::kSpill + lane;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const bool kept = (keep >> i) & 1u;
@@ -231,13 +243,16 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     }
     // bitmap byte: coordinate 8l+i is bit 7-i of byte 7 - l%8 of word l/8
     const uint32_t rev = __builtin_bitreverse32(keep) >> 24;
-    st[kCodeBytes + 8 * (lane >> 3) + 7 - (lane & 7)] = (uint8_t)rev;
-    if ((lane & 7) == 0) st[kDataBytes + (lane >> 3)] = (uint8_t)(e + 127);
+    st[kK + 8 * (lane >> 3) + 7 - (lane & 7)] = (uint8_t)rev;
+    if ((lane & 7) == 0) st[kK + kBitmapBytes + (lane >> 3)] = (uint8_t)(e + 127);
     wave_lds_sync();
 
-    // the 328-byte record is 8-byte aligned: 41 lanes store 8 bytes each
-    uint8_t* dst = pool + (slot >> 6) * kPageBytes + (slot & 63) * kRecordBytes;
-    if (lane < kRecordBytes / 8) *(u32x2*)(dst + 8 * lane) = *(const u32x2*)(st + 8 * lane);
+    // the record is 8-byte aligned: one 8-byte store per lane (41 lanes for the
+    // 328-byte record; the 520-byte 448-survivor record needs a 65th piece)
+    uint8_t* dst = pool + (slot >> 6) * R::kPage + (slot & 63) * R::kBytes;
+    if (lane < R::kPieces) *(u32x2*)(dst + 8 * lane) = *(const u32x2*)(st + 8 * lane);
+    if (R::kPieces > 64 && lane < R::kPieces - 64)
+      *(u32x2*)(dst + 512 + 8 * lane) = *(const u32x2*)(st + 512 + 8 * lane);
     wave_lds_sync();
   }
 }
@@ -328,12 +343,32 @@ int grid_for(int64_t n) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+template <int kK>
+void launch_pack(bool bf16, const void* x, int64_t stride, const float* weight, float eps,
+                 const int32_t* slots, int64_t n, uint8_t* pool, int64_t rows, hipStream_t s) {
+  if (bf16)
+    hipLaunchKernelGGL((pack_rows_kernel<true, kK>), dim3(grid_for(n)), dim3(256), 0, s, x,
+                       stride, weight, eps, slots, n, pool, rows);
+  else
+    hipLaunchKernelGGL((pack_rows_kernel<false, kK>), dim3(grid_for(n)), dim3(256), 0, s, x,
+                       stride, weight, eps, slots, n, pool, rows);
+}
+
 }  // namespace
 
 extern "C" int rm_pack_rows(const void* x, int x_dtype, int64_t x_row_stride,
                             const float* weight, float eps, const int32_t* dst_slot, int64_t n,
                             uint8_t* pool, int64_t pool_pages, void* stream) {
+  return rm_pack_rows_k(x, x_dtype, x_row_stride, weight, eps, dst_slot, n, pool, pool_pages,
+                        RM_KEEP_COUNT, stream);
+}
+
+extern "C" int rm_pack_rows_k(const void* x, int x_dtype, int64_t x_row_stride,
+                              const float* weight, float eps, const int32_t* dst_slot,
+                              int64_t n, uint8_t* pool, int64_t pool_pages, int keep_count,
+                              void* stream) {
   if (n < 0 || pool_pages < 0) return RM_ERR_SHAPE;
+  if (keep_count < 64 || keep_count > 448 || keep_count % 64) return RM_ERR_SHAPE;
   if (n == 0) return RM_OK;
   if (!x || !weight || !dst_slot || !pool) return RM_ERR_NULL;
   if (x_dtype != RM_F32 && x_dtype != RM_BF16) return RM_ERR_DTYPE;
@@ -344,12 +379,16 @@ extern "C" int rm_pack_rows(const void* x, int x_dtype, int64_t x_row_stride,
     return RM_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
   const int64_t rows = pool_pages * kPageRecords;
-  if (x_dtype == RM_BF16)
-    hipLaunchKernelGGL(pack_rows_kernel<true>, dim3(grid_for(n)), dim3(256), 0, s, x,
-                       x_row_stride, weight, eps, dst_slot, n, pool, rows);
-  else
-    hipLaunchKernelGGL(pack_rows_kernel<false>, dim3(grid_for(n)), dim3(256), 0, s, x,
-                       x_row_stride, weight, eps, dst_slot, n, pool, rows);
+  const bool bf16 = x_dtype == RM_BF16;
+  switch (keep_count) {
+    case 64: launch_pack<64>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
+    case 128: launch_pack<128>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
+    case 192: launch_pack<192>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
+    case 256: launch_pack<256>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
+    case 320: launch_pack<320>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
+    case 384: launch_pack<384>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
+    default: launch_pack<448>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
+  }
   return hipGetLastError() == hipSuccess ? RM_OK : RM_ERR_LAUNCH;
 }
 

@@ -29,10 +29,13 @@ _i64, _i32, _f32, _vp, _sz = (ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctyp
 SIGNATURES = {
     "rm_version": (_i32, []),
     "rm_pack_rows": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _vp, _i64, _vp]),
+    "rm_pack_rows_k": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _vp, _i64, _i32, _vp]),
     "rm_native_store_rows": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _vp,
                                     _i64, _vp]),
     "rm_unpack_gather_bf16": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
                                      _i64, _i64, _vp, _i64, _vp, _vp]),
+    "rm_unpack_gather_bf16_k": (_i32, [_vp, _i64, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp,
+                                       _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
     "rm_sparse_decode_workspace": (_i32, [_i64, _i64, _i64, ctypes.POINTER(ctypes.c_int32),
                                           ctypes.POINTER(ctypes.c_size_t)]),
     "rm_remnant_sparse_decode_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64,

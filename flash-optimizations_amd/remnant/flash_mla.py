@@ -32,9 +32,12 @@ def get_decode_metadata(tokens: int, heads: int, topk: int) -> tuple[int, int]:
 
 def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length, sink,
             freqs_cis, softmax_scale, out, lse, workspace, layer_id):
-    buf, is_packed = _as_pool(pool, layer_id)
+    buf, is_packed, keep = _as_pool(pool, layer_id)
     if is_packed != packed:
         raise ValueError("pool format does not match the decode reader")
+    if packed and keep != config.KEEP_COUNT:
+        raise ValueError("the Direct decode reader reads 256-survivor records only; use "
+                         "unpack_gather_bf16 for other survivor counts")
     if q.dim() != 4 or q.shape[-1] != config.HEAD_DIM or q.dtype != torch.bfloat16 \
             or not q.is_contiguous():
         raise ValueError("q must be a contiguous bfloat16 [batch, q_len, heads, 512] tensor")

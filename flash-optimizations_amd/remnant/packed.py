@@ -20,17 +20,19 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-def _as_pool(buffers, layer_id) -> tuple[torch.Tensor, bool]:
-    """Resolve a LatentPool (+ layer) or a raw uint8 page tensor [pages, page_bytes]."""
+def _as_pool(buffers, layer_id) -> tuple[torch.Tensor, bool, int]:
+    """Resolve a LatentPool (+ layer) or a raw uint8 page tensor [pages, page_bytes]
+    to (pages, packed, survivor count); a raw tensor's page size names its format."""
     if isinstance(buffers, LatentPool):
-        return buffers.layer(layer_id), buffers.packed
+        return buffers.layer(layer_id), buffers.packed, buffers.keep_count
     if isinstance(buffers, torch.Tensor):
         if buffers.dtype != torch.uint8 or buffers.dim() != 2 or not buffers.is_contiguous():
             raise ValueError("pool must be a contiguous uint8 [pages, page_bytes] tensor")
-        if buffers.shape[1] == config.PACKED_PAGE_BYTES:
-            return buffers, True
         if buffers.shape[1] == config.NATIVE_PAGE_BYTES:
-            return buffers, False
+            return buffers, False, config.KEEP_COUNT
+        keep = config.keep_count_of_page_bytes(buffers.shape[1])
+        if keep is not None:
+            return buffers, True, keep
         raise ValueError(f"unknown page size {buffers.shape[1]}")
     raise ValueError("packed_buffers must be a LatentPool or a uint8 page tensor")
 
@@ -45,8 +47,9 @@ def pack_rows_fused(x: torch.Tensor, weight: torch.Tensor, eps: float, loc: torc
                     pool, *, layer_id: int | None = None) -> None:
     """Pack raw C4 rows ``x`` [n, 512] (float32 compressor output or bfloat16)
     into Packed records at pool slots ``loc`` [n] int32 (slots outside the
-    pool are skipped)."""
-    buf, packed = _as_pool(pool, layer_id)
+    pool are skipped). The pool's survivor count (256 by default) sets how many
+    coordinates each record keeps."""
+    buf, packed, keep = _as_pool(pool, layer_id)
     if not packed:
         raise ValueError("pack_rows_fused writes the Packed (remnant) format")
     if x.dim() != 2 or x.shape[-1] != config.HEAD_DIM or x.stride(-1) != 1:
@@ -61,9 +64,9 @@ def pack_rows_fused(x: torch.Tensor, weight: torch.Tensor, eps: float, loc: torc
         return
     _check_cuda(x, weight, loc, buf)
     dtype = 1 if x.dtype == torch.bfloat16 else 0
-    _lib.check(_lib.load().rm_pack_rows(
+    _lib.check(_lib.load().rm_pack_rows_k(
         x.data_ptr(), dtype, x.stride(0), weight.data_ptr(), float(eps), loc.data_ptr(),
-        x.shape[0], buf.data_ptr(), buf.shape[0], _stream()), "rm_pack_rows")
+        x.shape[0], buf.data_ptr(), buf.shape[0], keep, _stream()), "rm_pack_rows_k")
 
 
 def native_store_rows(x: torch.Tensor, weight: torch.Tensor, eps: float, loc: torch.Tensor,
@@ -71,7 +74,7 @@ def native_store_rows(x: torch.Tensor, weight: torch.Tensor, eps: float, loc: to
                       *, layer_id: int | None = None) -> None:
     """Native 584-byte control store (unpruned RMSNorm, tail rotated with
     frequency row positions * 4)."""
-    buf, packed = _as_pool(pool, layer_id)
+    buf, packed, _ = _as_pool(pool, layer_id)
     if packed:
         raise ValueError("native_store_rows writes the Native format")
     if x.dim() != 2 or x.shape[-1] != config.HEAD_DIM or x.stride(-1) != 1:
@@ -116,7 +119,7 @@ def unpack_gather_bf16(packed_buffers, physical_indices: torch.Tensor,
     """
     if type(fused_rope) is not bool:
         raise TypeError("fused_rope must be a bool")
-    buf, packed = _as_pool(packed_buffers, layer_id)
+    buf, packed, keep = _as_pool(packed_buffers, layer_id)
     if not packed:
         raise ValueError("unpack_gather_bf16 reads the Packed (remnant) format")
     if raw_indices is not None and physical_indices.shape != raw_indices.shape:
@@ -148,13 +151,13 @@ def unpack_gather_bf16(packed_buffers, physical_indices: torch.Tensor,
     if n_queries * selected_k == 0:
         return output
     _check_cuda(buf, physical_indices, raw_indices, topk_lengths, output, freqs_cis)
-    _lib.check(_lib.load().rm_unpack_gather_bf16(
-        buf.data_ptr(), buf.shape[0], physical_indices.data_ptr(), physical_indices.stride(0),
+    _lib.check(_lib.load().rm_unpack_gather_bf16_k(
+        buf.data_ptr(), buf.shape[0], keep, physical_indices.data_ptr(), physical_indices.stride(0),
         physical_indices.stride(1), None if raw_indices is None else raw_indices.data_ptr(),
         0 if raw_indices is None else raw_indices.stride(0),
         0 if raw_indices is None else raw_indices.stride(1), topk_lengths.data_ptr(),
         topk_lengths.stride(0), n_queries, selected_k, freq_ptr, freq_rows, output.data_ptr(),
-        _stream()), "rm_unpack_gather_bf16")
+        _stream()), "rm_unpack_gather_bf16_k")
     return output
 
 

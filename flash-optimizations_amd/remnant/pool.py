@@ -13,6 +13,11 @@ rows of 576 bytes, then 64 scale rows of 8 bytes (the tail read
 ``native[page, value_base + 448 : value_base + 576]``, candidate-sglang.patch:701). The reference's planes are exposed as strided views of the
 same memory (no copies), which is what a host-cache transfer or an inspection
 needs.
+
+A Packed pool may hold a survivor profile other than 256 (``keep_count`` 64..448
+in steps of 64, docs/agents/numerical-and-validation.md:10-14): its records are
+``keep_count + 72`` bytes with the same code/bitmap/scale order, 64 to a page.
+One pool holds one profile; per-layer profiles use one pool per layer.
 """
 
 from __future__ import annotations
@@ -23,18 +28,27 @@ from . import config
 
 
 class LatentPool:
-    def __init__(self, pages: int, layers: int = 1, fmt: str = "remnant", device="cuda"):
+    def __init__(self, pages: int, layers: int = 1, fmt: str = "remnant", device="cuda",
+                 keep_count: int = config.KEEP_COUNT):
         if fmt == "direct":
             fmt = "remnant"
         if fmt not in ("remnant", "native"):
             raise ValueError(f"unsupported cache format: {fmt!r}")
         if pages < 0 or layers < 1:
             raise ValueError("pages must be >= 0 and layers >= 1")
+        config.check_keep_count(keep_count)
+        if fmt == "native" and keep_count != config.KEEP_COUNT:
+            raise ValueError("Native records keep every coordinate; keep_count is Packed-only")
         self.fmt = fmt
         self.pages = pages
         self.layers = layers
-        self.page_bytes = config.PACKED_PAGE_BYTES if fmt == "remnant" else config.NATIVE_PAGE_BYTES
-        self.data_bytes = config.PACKED_DATA_BYTES if fmt == "remnant" else config.NATIVE_DATA_BYTES
+        self.keep_count = keep_count
+        if fmt == "remnant":
+            self.page_bytes = config.packed_page_bytes(keep_count)
+            self.data_bytes = keep_count + 8 * config.BITMAP_WORDS
+        else:
+            self.page_bytes = config.NATIVE_PAGE_BYTES
+            self.data_bytes = config.NATIVE_DATA_BYTES
         self.buffer = torch.zeros((layers, pages, self.page_bytes), dtype=torch.uint8,
                                   device=device)
 
@@ -54,9 +68,9 @@ class LatentPool:
         return self.buffer[0 if layer_id is None else layer_id]
 
     def _data_rows(self, layer_id):
-        if self.packed:  # contiguous records: data = first 320 bytes of each
+        if self.packed:  # contiguous records: data = all but the last 8 bytes of each
             pg = self.layer(layer_id).reshape(self.pages, config.PAGE_RECORDS,
-                                              config.PACKED_RECORD_BYTES)
+                                              self.record_bytes)
             return pg[..., : self.data_bytes]
         pg = self.layer(layer_id)[:, : config.PAGE_RECORDS * self.data_bytes]
         return pg.reshape(self.pages, config.PAGE_RECORDS, self.data_bytes)
@@ -65,21 +79,21 @@ class LatentPool:
         """Scale plane view [pages, 64, 8] u8."""
         if self.packed:
             pg = self.layer(layer_id).reshape(self.pages, config.PAGE_RECORDS,
-                                              config.PACKED_RECORD_BYTES)
+                                              self.record_bytes)
             return pg[..., self.data_bytes:]
         pg = self.layer(layer_id)[:, config.PAGE_RECORDS * self.data_bytes:]
         return pg.reshape(self.pages, config.PAGE_RECORDS, 8)
 
     def values(self, layer_id: int | None = None) -> torch.Tensor:
-        """Code plane view: Packed [pages, 64, 256] u8, Native [pages, 64, 448] u8."""
-        width = config.KEEP_COUNT if self.packed else config.NOPE_DIM
+        """Code plane view: Packed [pages, 64, keep_count] u8, Native [pages, 64, 448] u8."""
+        width = self.keep_count if self.packed else config.NOPE_DIM
         return self._data_rows(layer_id)[..., :width]
 
     def bitmaps(self, layer_id: int | None = None) -> torch.Tensor:
         """Bitmap plane view [pages, 64, 64] u8 (8 little-endian MSB-first uint64 words)."""
         if not self.packed:
             raise ValueError("Native records carry no bitmap")
-        return self._data_rows(layer_id)[..., config.KEEP_COUNT:config.PACKED_DATA_BYTES]
+        return self._data_rows(layer_id)[..., self.keep_count:self.data_bytes]
 
     def records(self, slots: torch.Tensor, layer_id: int | None = None) -> torch.Tensor:
         """Logical records [n, record_bytes] (data row + scale row) for pool slots."""
@@ -95,8 +109,8 @@ class LatentPool:
         return self.buffer.numel()
 
 
-def records_fitting(nbytes: int, fmt: str = "remnant") -> int:
-    """Whole pages of records that fit in ``nbytes`` of HBM."""
+def records_fitting(nbytes: int, fmt: str = "remnant", keep_count: int = config.KEEP_COUNT) -> int:
+    """Records (whole pages of 64) that fit in ``nbytes`` of HBM."""
     fmt = "remnant" if fmt == "direct" else fmt
-    page = config.PACKED_PAGE_BYTES if fmt == "remnant" else config.NATIVE_PAGE_BYTES
+    page = config.packed_page_bytes(keep_count) if fmt == "remnant" else config.NATIVE_PAGE_BYTES
     return (nbytes // page) * config.PAGE_RECORDS

@@ -33,6 +33,16 @@
  *                             stock FlashMLA sparse FP8 decode on 584-B records
  *                             (Native control, same harness)
  *   rm_sparse_decode_workspace  FlashMLA get_mla_metadata-style split planning
+ *   rm_pack_rows_k / rm_unpack_gather_bf16_k
+ *                             the survivor-profile store and reader
+ *                             (configure_cache_format(..., keep_count=K) with the
+ *                             KEEP_K Triton kernels: candidate-sglang.patch:471-479,
+ *                             707-736, 775-790; docs/agents/numerical-and-validation.md:10-14)
+ *
+ * Survivor profiles: a Packed pool may instead hold records with K survivors,
+ * K = 64..448 in steps of 64: K E4M3 codes, the same 64 bitmap bytes and 8 scale
+ * bytes (K + 72 bytes, 8-byte aligned), 64 records per page (64 * (K + 72) B).
+ * The sparse decode reads the 256-survivor format only.
  */
 #ifndef REMNANT_MI355X_H
 #define REMNANT_MI355X_H
@@ -81,6 +91,13 @@ int rm_pack_rows(const void* x, int x_dtype, int64_t x_row_stride, const float* 
                  float eps, const int32_t* dst_slot, int64_t n, uint8_t* pool,
                  int64_t pool_pages, void* stream);
 
+/* rm_pack_rows for a pool of keep_count-survivor records (keep_count 64..448,
+ * a multiple of 64; other values give RM_ERR_SHAPE). rm_pack_rows is this
+ * entry point with keep_count 256. */
+int rm_pack_rows_k(const void* x, int x_dtype, int64_t x_row_stride, const float* weight,
+                   float eps, const int32_t* dst_slot, int64_t n, uint8_t* pool,
+                   int64_t pool_pages, int keep_count, void* stream);
+
 /* Native control store: unpruned RMSNorm, 7 NoPE groups as UE8M0/E4M3, tail
  * rotated with freqs row position[i] * 4 (freqs: [freq_rows, 32] complex64 as
  * interleaved f32 (cos, sin); NULL = no rotation). Rows whose slot is out of
@@ -101,6 +118,16 @@ int rm_unpack_gather_bf16(const uint8_t* pool, int64_t pool_pages, const int32_t
                           const int32_t* lengths, int64_t length_stride, int64_t n_queries,
                           int64_t selected_k, const float* freqs, int64_t freq_rows,
                           uint16_t* out, void* stream);
+
+/* rm_unpack_gather_bf16 on a pool of keep_count-survivor records (keep_count
+ * 64..448, a multiple of 64; other values give RM_ERR_SHAPE). */
+int rm_unpack_gather_bf16_k(const uint8_t* pool, int64_t pool_pages, int keep_count,
+                            const int32_t* physical, int64_t physical_stride_q,
+                            int64_t physical_stride_k, const int32_t* raw,
+                            int64_t raw_stride_q, int64_t raw_stride_k,
+                            const int32_t* lengths, int64_t length_stride, int64_t n_queries,
+                            int64_t selected_k, const float* freqs, int64_t freq_rows,
+                            uint16_t* out, void* stream);
 
 /* Split planning for the sparse decode of `tokens` query tokens with `topk`
  * selected records each and `heads` query heads. Writes the number of split-KV

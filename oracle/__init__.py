@@ -32,6 +32,16 @@ PAGE_BYTES = PAGE_RECORDS * RECORD_BYTES
 NATIVE_DATA_BYTES = 576
 NATIVE_RECORD_BYTES = NATIVE_DATA_BYTES + SCALE_BYTES
 NATIVE_PAGE_BYTES = PAGE_RECORDS * NATIVE_RECORD_BYTES
+KEEP_COUNTS = tuple(range(64, 512, 64))  # survivor profiles 64..448
+
+
+def record_bytes(keep_count: int = KEEP) -> int:
+    """Bytes of one Packed record with ``keep_count`` survivors (count + 72)."""
+    return keep_count + 64 + SCALE_BYTES
+
+
+def page_bytes(keep_count: int = KEEP) -> int:
+    return PAGE_RECORDS * record_bytes(keep_count)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
@@ -62,6 +72,12 @@ def lib():
         _lib.orc_rms_scale.restype = f32
         _lib.orc_rms_scale.argtypes = [f32, f32]
         _lib.orc_select_keep.argtypes = [vp, vp]
+        _lib.orc_select_keep_k.argtypes = [vp, vp, ctypes.c_int]
+        _lib.orc_pack_row_k.argtypes = [vp, vp, f32, ctypes.c_int, vp, vp, vp, vp]
+        _lib.orc_pack_rows_paged_k.argtypes = [vp, vp, f32, ctypes.c_int, vp, i64, vp, i64]
+        _lib.orc_unpack_row_k.argtypes = [vp, vp, ctypes.c_int, vp]
+        _lib.orc_unpack_gather_k.argtypes = [vp, i64, ctypes.c_int, vp, i64, i64, vp, i64,
+                                             i64, vp, i64, i64, i64, vp, i64, vp]
         _lib.orc_normalize.argtypes = [vp, vp, vp, f32, vp]
         _lib.orc_simulate_rows.argtypes = [vp, vp, vp, f32, i64, vp]
         _lib.orc_pack_row.argtypes = [vp, vp, f32, vp, vp, vp, vp]
@@ -123,12 +139,19 @@ def ue8m0_exponent(amax: float) -> int:
 
 # ---- rows ------------------------------------------------------------------
 
-def select_keep(x) -> np.ndarray:
-    """[rows, 512] float32 -> bool keep mask, 256 per row."""
+def _check_keep(keep_count: int) -> int:
+    if keep_count not in KEEP_COUNTS:
+        raise ValueError(f"keep_count must be one of {KEEP_COUNTS}")
+    return keep_count
+
+
+def select_keep(x, keep_count: int = KEEP) -> np.ndarray:
+    """[rows, 512] float32 -> bool keep mask, keep_count per row."""
+    _check_keep(keep_count)
     x = _c(x, np.float32).reshape(-1, HEAD_DIM)
     out = np.zeros(x.shape, dtype=np.uint8)
     for r in range(x.shape[0]):
-        lib().orc_select_keep(_p(x[r]), _p(out[r]))
+        lib().orc_select_keep_k(_p(x[r]), _p(out[r]), keep_count)
     return out.astype(bool)
 
 
@@ -154,44 +177,49 @@ def simulate_rows(x, keep, weight, eps: float) -> np.ndarray:
     return out
 
 
-def pack_rows(x, weight, eps: float):
-    """Records in row order: data [rows, 320] u8, scales [rows, 8] u8,
-    normalized bf16 bits [rows, 512], keep mask [rows, 512]."""
+def pack_rows(x, weight, eps: float, keep_count: int = KEEP):
+    """Records in row order: data [rows, keep_count + 64] u8 (codes, bitmap),
+    scales [rows, 8] u8, normalized bf16 bits [rows, 512], keep mask [rows, 512]."""
+    _check_keep(keep_count)
     x = _c(x, np.float32).reshape(-1, HEAD_DIM)
     w = _c(weight, np.float32)
     n = x.shape[0]
-    data = np.zeros((n, DATA_BYTES), np.uint8)
+    data = np.zeros((n, keep_count + 64), np.uint8)
     scales = np.zeros((n, SCALE_BYTES), np.uint8)
     normed = np.zeros((n, HEAD_DIM), np.uint16)
     keep = np.zeros((n, HEAD_DIM), np.uint8)
     for r in range(n):
-        lib().orc_pack_row(_p(x[r]), _p(w), eps, _p(data[r]), _p(scales[r]), _p(normed[r]),
-                           _p(keep[r]))
+        lib().orc_pack_row_k(_p(x[r]), _p(w), eps, keep_count, _p(data[r]), _p(scales[r]),
+                             _p(normed[r]), _p(keep[r]))
     return data, scales, normed, keep.astype(bool)
 
 
-def pack_rows_paged(x, weight, eps: float, slots, pool: np.ndarray) -> np.ndarray:
-    """Pack rows into a paged pool (uint8 [pages, 20992]) in place."""
+def pack_rows_paged(x, weight, eps: float, slots, pool: np.ndarray,
+                    keep_count: int = KEEP) -> np.ndarray:
+    """Pack rows into a paged pool (uint8 [pages, 64 * (keep_count + 72)]) in place."""
+    _check_keep(keep_count)
     x = _c(x, np.float32).reshape(-1, HEAD_DIM)
     s = _c(slots, np.int32)
     assert pool.dtype == np.uint8 and pool.flags.c_contiguous
-    pages = pool.size // PAGE_BYTES
-    lib().orc_pack_rows_paged(_p(x), _p(_c(weight, np.float32)), eps, _p(s), x.shape[0],
-                              _p(pool), pages)
+    pages = pool.size // page_bytes(keep_count)
+    lib().orc_pack_rows_paged_k(_p(x), _p(_c(weight, np.float32)), eps, keep_count, _p(s),
+                                x.shape[0], _p(pool), pages)
     return pool
 
 
-def unpack_row(data, scales) -> np.ndarray:
+def unpack_row(data, scales, keep_count: int = KEEP) -> np.ndarray:
+    _check_keep(keep_count)
     out = np.zeros(HEAD_DIM, np.uint16)
-    lib().orc_unpack_row(_p(_c(data, np.uint8)), _p(_c(scales, np.uint8)), _p(out))
+    lib().orc_unpack_row_k(_p(_c(data, np.uint8)), _p(_c(scales, np.uint8)), keep_count,
+                           _p(out))
     return out
 
 
-def unpack_rows(data, scales) -> np.ndarray:
-    data = _c(data, np.uint8).reshape(-1, DATA_BYTES)
+def unpack_rows(data, scales, keep_count: int = KEEP) -> np.ndarray:
+    data = _c(data, np.uint8).reshape(-1, keep_count + 64)
     scales = _c(scales, np.uint8).reshape(-1, SCALE_BYTES)
-    return np.stack([unpack_row(d, s) for d, s in zip(data, scales)]) if len(data) else \
-        np.zeros((0, HEAD_DIM), np.uint16)
+    return np.stack([unpack_row(d, s, keep_count) for d, s in zip(data, scales)]) \
+        if len(data) else np.zeros((0, HEAD_DIM), np.uint16)
 
 
 def rope_tail(row_bits, freq_row) -> np.ndarray:
@@ -203,8 +231,10 @@ def rope_tail(row_bits, freq_row) -> np.ndarray:
     return rows
 
 
-def unpack_gather(pool, physical, raw, lengths, freqs=None) -> np.ndarray:
-    """unpack_gather_bf16 on a paged pool: returns bf16 bits [Q*K, 512]."""
+def unpack_gather(pool, physical, raw, lengths, freqs=None, keep_count: int = KEEP) -> np.ndarray:
+    """unpack_gather_bf16 on a paged pool of ``keep_count``-survivor records:
+    returns bf16 bits [Q*K, 512]."""
+    _check_keep(keep_count)
     pool = _c(pool, np.uint8)
     phys = np.asarray(physical, np.int32)
     raw_a = None if raw is None else np.asarray(raw, np.int32)
@@ -213,9 +243,9 @@ def unpack_gather(pool, physical, raw, lengths, freqs=None) -> np.ndarray:
     out = np.zeros((nq * nk, HEAD_DIM), np.uint16)
     f = None if freqs is None else _c(freqs, np.float32)
     phys_c, raw_c = _c(phys, np.int32), None if raw_a is None else _c(raw_a, np.int32)
-    lib().orc_unpack_gather(_p(pool), pool.size // PAGE_BYTES, _p(phys_c), nk, 1,
-                            _p(raw_c), nk, 1, _p(lens), 1, nq, nk, _p(f),
-                            0 if f is None else f.size // (ROPE_PAIRS * 2), _p(out))
+    lib().orc_unpack_gather_k(_p(pool), pool.size // page_bytes(keep_count), keep_count,
+                              _p(phys_c), nk, 1, _p(raw_c), nk, 1, _p(lens), 1, nq, nk, _p(f),
+                              0 if f is None else f.size // (ROPE_PAIRS * 2), _p(out))
     return out
 
 

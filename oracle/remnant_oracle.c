@@ -14,7 +14,8 @@
  *   UE8M0 + E4M3   training/losses.py:90-94; closed form at
  *                  training/tests/test_integration.py:1588-1619
  *   record         docs/agents/numerical-and-validation.md:10-12 (256 + 64 + 8 bytes),
- *                  planes at candidate-sglang.patch:900-904
+ *                  planes at candidate-sglang.patch:900-904; other survivor counts
+ *                  64..448 in steps of 64 take count + 72 bytes (same doc, :11-14)
  *   unpack + RoPE  candidate-sglang.patch:502-588 (gather/dequant/zero rows),
  *                  :640-668 (bf16 round, pair rotation, raw*4 frequency row)
  *   native record  training/tests/test_integration.py:361-367 (584-byte layout)
@@ -29,9 +30,11 @@
  *     (distance 1, 2, 4, ... 32);
  *   - rsqrt(v) = RN(1 / RN(sqrt(v))); (m * r) * w are two rounded products;
  *   - bitmap words are MSB-first: coordinate c is bit 63 - (c % 64) of word c/64;
+ *   - ties at the K/K+1 boundary of a K-survivor profile likewise;
  *   - a Packed page holds 64 contiguous 328-byte records (codes, bitmap,
- *     scales); a Native page holds the 64 data rows (576 bytes) followed by
- *     the 64 scale rows (8 bytes), matching the reference's Native tail read
+ *     scales), or (K + 72)-byte records for K survivors; a Native page holds
+ *     the 64 data rows (576 bytes) followed by the 64 scale rows (8 bytes),
+ *     matching the reference's Native tail read
  *     native[page, value_base + 448 : value_base + 576] (candidate-sglang.patch:701);
  *   - the RoPE pair rotation is re = RN(RN(xr*c) - RN(xi*s)),
  *     im = RN(RN(xr*s) + RN(xi*c)), on BF16-rounded inputs.
@@ -107,21 +110,24 @@ static int cmp_desc_u32(const void* a, const void* b) {
     return x < y ? 1 : (x > y ? -1 : 0);
 }
 
-/* Keep the 256 largest |x| of 512; ties at the boundary keep lower coordinates. */
-void orc_select_keep(const float* x, uint8_t* keep) {
+/* Keep the K largest |x| of 512 (K = 64..448 in steps of 64; 256 is the
+ * default profile); ties at the boundary keep lower coordinates. */
+void orc_select_keep_k(const float* x, uint8_t* keep, int K) {
     uint32_t key[HEAD_DIM], sorted[HEAD_DIM];
     for (int c = 0; c < HEAD_DIM; ++c) sorted[c] = key[c] = f2u(x[c]) & 0x7fffffffu;
     qsort(sorted, HEAD_DIM, sizeof(uint32_t), cmp_desc_u32);
-    uint32_t t = sorted[KEEP - 1];
+    uint32_t t = sorted[K - 1];
     int gt = 0;
     for (int c = 0; c < HEAD_DIM; ++c) gt += key[c] > t;
-    int ties = KEEP - gt;
+    int ties = K - gt;
     for (int c = 0; c < HEAD_DIM; ++c) {
         if (key[c] > t) keep[c] = 1;
         else if (key[c] == t && ties > 0) { keep[c] = 1; --ties; }
         else keep[c] = 0;
     }
 }
+
+void orc_select_keep(const float* x, uint8_t* keep) { orc_select_keep_k(x, keep, KEEP); }
 
 /* Sum of squares in the kernel's fixed order (see header). */
 float orc_sumsq(const float* m) {
@@ -194,50 +200,71 @@ void orc_simulate_rows(const float* x, const uint8_t* keep, const float* w, floa
     }
 }
 
-/* Pack one record: data = 256 codes (ascending coordinate) + 8 MSB-first
- * uint64 bitmap words (little-endian bytes); scales = 8 UE8M0 bytes. */
-void orc_pack_row(const float* x, const float* w, float eps, uint8_t* data,
-                  uint8_t* scales, uint16_t* normalized_out, uint8_t* keep_out) {
+/* Pack one record with K survivors: data = K codes (ascending coordinate) +
+ * 8 MSB-first uint64 bitmap words (little-endian bytes); scales = 8 UE8M0
+ * bytes. A K-survivor record is K + 72 bytes (codes, bitmap, scales). */
+void orc_pack_row_k(const float* x, const float* w, float eps, int K, uint8_t* data,
+                    uint8_t* scales, uint16_t* normalized_out, uint8_t* keep_out) {
     uint8_t keep[HEAD_DIM], codes[HEAD_DIM];
     uint16_t n[HEAD_DIM];
-    orc_select_keep(x, keep);
+    orc_select_keep_k(x, keep, K);
     orc_normalize(x, keep, w, eps, n);
     quantize_groups(n, 0, NGROUPS, codes, scales);
     int rank = 0;
-    memset(data, 0, DATA_BYTES);
+    memset(data, 0, K + BITMAP_BYTES);
     for (int c = 0; c < HEAD_DIM; ++c) {
         if (!keep[c]) continue;
         data[rank++] = codes[c];
         int word = c / 64, bit = 63 - (c % 64);
-        data[CODE_BYTES + word * 8 + bit / 8] |= (uint8_t)(1u << (bit % 8));
+        data[K + word * 8 + bit / 8] |= (uint8_t)(1u << (bit % 8));
     }
     if (normalized_out) memcpy(normalized_out, n, sizeof(n));
     if (keep_out) memcpy(keep_out, keep, sizeof(keep));
 }
 
+void orc_pack_row(const float* x, const float* w, float eps, uint8_t* data,
+                  uint8_t* scales, uint16_t* normalized_out, uint8_t* keep_out) {
+    orc_pack_row_k(x, w, eps, KEEP, data, scales, normalized_out, keep_out);
+}
+
 static inline int64_t page_of(int64_t slot) { return slot / PAGE_RECORDS; }
 
+/* Record bytes and page bytes of the K-survivor Packed format. */
+static inline int64_t record_bytes_k(int K) { return K + BITMAP_BYTES + SCALE_BYTES; }
+static inline int64_t page_bytes_k(int K) { return PAGE_RECORDS * record_bytes_k(K); }
+
 /* Pack rows into the paged pool at dst_slot[i] (negative slots are skipped). */
-void orc_pack_rows_paged(const float* x, const float* w, float eps, const int32_t* slot,
-                         int64_t rows, uint8_t* pool, int64_t pool_pages) {
+void orc_pack_rows_paged_k(const float* x, const float* w, float eps, int K,
+                           const int32_t* slot, int64_t rows, uint8_t* pool,
+                           int64_t pool_pages) {
+    const int64_t rb = record_bytes_k(K), pb = page_bytes_k(K);
     for (int64_t i = 0; i < rows; ++i) {
         int64_t s = slot[i];
         if (s < 0 || s >= pool_pages * PAGE_RECORDS) continue;
-        uint8_t* rec = pool + page_of(s) * PAGE_BYTES + (s % PAGE_RECORDS) * RECORD_BYTES;
-        orc_pack_row(x + i * HEAD_DIM, w, eps, rec, rec + DATA_BYTES, NULL, NULL);
+        uint8_t* rec = pool + page_of(s) * pb + (s % PAGE_RECORDS) * rb;
+        orc_pack_row_k(x + i * HEAD_DIM, w, eps, K, rec, rec + K + BITMAP_BYTES, NULL, NULL);
     }
 }
 
-/* Dequantize one record to pre-RoPE BF16 (exact). */
-void orc_unpack_row(const uint8_t* data, const uint8_t* scales, uint16_t* out) {
+void orc_pack_rows_paged(const float* x, const float* w, float eps, const int32_t* slot,
+                         int64_t rows, uint8_t* pool, int64_t pool_pages) {
+    orc_pack_rows_paged_k(x, w, eps, KEEP, slot, rows, pool, pool_pages);
+}
+
+/* Dequantize one K-survivor record to pre-RoPE BF16 (exact). */
+void orc_unpack_row_k(const uint8_t* data, const uint8_t* scales, int K, uint16_t* out) {
     int rank = 0;
     for (int c = 0; c < HEAD_DIM; ++c) {
         int word = c / 64, bit = 63 - (c % 64);
-        int kept = (data[CODE_BYTES + word * 8 + bit / 8] >> (bit % 8)) & 1;
+        int kept = (data[K + word * 8 + bit / 8] >> (bit % 8)) & 1;
         if (!kept) { out[c] = 0; continue; }
         float v = orc_e4m3_decode(data[rank++]) * ldexpf(1.0f, (int)scales[c / GROUP] - 127);
         out[c] = orc_f32_to_bf16(v);
     }
+}
+
+void orc_unpack_row(const uint8_t* data, const uint8_t* scales, uint16_t* out) {
+    orc_unpack_row_k(data, scales, KEEP, out);
 }
 
 /* In-place tail rotation of a BF16 row with one complex frequency row
@@ -257,12 +284,15 @@ void orc_rope_tail(uint16_t* row, const float* freq) {
 /* unpack_gather_bf16 (candidate-sglang.patch:427-480, 502-668): row (q, k)
  * gathers pool slot physical[q, k]; it is zero unless k < lengths[q],
  * 0 <= physical < pool rows and, with a frequency table, 0 <= raw*4 < freq_rows.
- * freqs == NULL selects the pre-RoPE reader (raw unused). */
-void orc_unpack_gather(const uint8_t* pool, int64_t pool_pages, const int32_t* physical,
-                       int64_t ps_q, int64_t ps_k, const int32_t* raw, int64_t rs_q,
-                       int64_t rs_k, const int32_t* lengths, int64_t ls, int64_t nq,
-                       int64_t nk, const float* freqs, int64_t freq_rows, uint16_t* out) {
+ * freqs == NULL selects the pre-RoPE reader (raw unused). K is the pool's
+ * survivor count (its records are K + 72 bytes). */
+void orc_unpack_gather_k(const uint8_t* pool, int64_t pool_pages, int K,
+                         const int32_t* physical, int64_t ps_q, int64_t ps_k,
+                         const int32_t* raw, int64_t rs_q, int64_t rs_k,
+                         const int32_t* lengths, int64_t ls, int64_t nq, int64_t nk,
+                         const float* freqs, int64_t freq_rows, uint16_t* out) {
     int64_t rows = pool_pages * PAGE_RECORDS;
+    const int64_t rb = record_bytes_k(K), pb = page_bytes_k(K);
     for (int64_t q = 0; q < nq; ++q)
         for (int64_t k = 0; k < nk; ++k) {
             uint16_t* o = out + (q * nk + k) * HEAD_DIM;
@@ -271,10 +301,18 @@ void orc_unpack_gather(const uint8_t* pool, int64_t pool_pages, const int32_t* p
             int valid = k < lengths[q * ls] && p >= 0 && p < rows;
             if (freqs) valid = valid && r >= 0 && r * 4 < freq_rows;
             if (!valid) { memset(o, 0, HEAD_DIM * 2); continue; }
-            const uint8_t* rec = pool + page_of(p) * PAGE_BYTES + (p % PAGE_RECORDS) * RECORD_BYTES;
-            orc_unpack_row(rec, rec + DATA_BYTES, o);
+            const uint8_t* rec = pool + page_of(p) * pb + (p % PAGE_RECORDS) * rb;
+            orc_unpack_row_k(rec, rec + K + BITMAP_BYTES, K, o);
             if (freqs) orc_rope_tail(o, freqs + r * 4 * ROPE_PAIRS * 2);
         }
+}
+
+void orc_unpack_gather(const uint8_t* pool, int64_t pool_pages, const int32_t* physical,
+                       int64_t ps_q, int64_t ps_k, const int32_t* raw, int64_t rs_q,
+                       int64_t rs_k, const int32_t* lengths, int64_t ls, int64_t nq,
+                       int64_t nk, const float* freqs, int64_t freq_rows, uint16_t* out) {
+    orc_unpack_gather_k(pool, pool_pages, KEEP, physical, ps_q, ps_k, raw, rs_q, rs_k, lengths,
+                        ls, nq, nk, freqs, freq_rows, out);
 }
 
 /* Native 584-byte record: unpruned RMSNorm -> BF16; nope groups 0..6 as

@@ -70,6 +70,14 @@ def test_capi_rejects_bad_arguments_without_launching():
                                      None) == -1  # freqs without raw
     assert lib.rm_unpack_gather_bf16(pool, 1, s, 1, 1, None, 0, 0, s, 1, 2, 5, None, 0, x + 8,
                                      None) == -3
+    for bad in (0, 32, 200, 512, -64):  # survivor counts outside the profiles
+        assert lib.rm_pack_rows_k(x, 1, 512, w, 1e-6, s, 4, pool, 1, bad, None) == -2
+        assert lib.rm_unpack_gather_bf16_k(pool, 1, bad, s, 1, 1, None, 0, 0, s, 1, 2, 5, None,
+                                           0, x, None) == -2
+    assert lib.rm_pack_rows_k(x, 1, 512, w, 1e-6, s, 0, pool, 1, 448, None) == 0
+    assert lib.rm_pack_rows_k(None, 1, 512, w, 1e-6, s, 4, pool, 1, 64, None) == -1
+    assert lib.rm_unpack_gather_bf16_k(pool, 1, 192, s, 1, 1, None, 0, 0, s, 1, 0, 5, None, 0,
+                                       x, None) == 0
     args = [x, 1, 1, 17, pool, 1, s, 4, 4, None, s, 8, None, None, None, 0, 0.1, x, w, None, 0,
             None]
     assert lib.rm_remnant_sparse_decode_fwd(*args) == -2  # 17 heads
@@ -159,11 +167,24 @@ def test_cache_format_configuration():
         assert remnant.packed_profile()["record_bytes"] == 328
         assert not remnant.configure_cache_format("native").packed
         assert remnant.packed_profile()["record_bytes"] == 584
+        # the Direct reader is 256-only; 512 and non-multiples of 64 are no profile
+        # (docs/agents/numerical-and-validation.md:11-16)
         for bad in (dict(fmt="fp4"), dict(fmt="remnant", keep_count=192),
-                    dict(fmt="remnant", decode_impl="triton"),
-                    dict(fmt="remnant", layer_keep_counts=[256, 128])):
+                    dict(fmt="remnant", layer_keep_counts=[256, 128]),
+                    dict(fmt="remnant", decode_impl="triton", keep_count=512),
+                    dict(fmt="remnant", decode_impl="triton", keep_count=200),
+                    dict(fmt="remnant", decode_impl="triton", keep_count=192.0),
+                    dict(fmt="remnant", decode_impl="flashinfer"),
+                    dict(fmt="remnant", decode_impl="triton", layer_keep_counts=[256, 512])):
             with pytest.raises(ValueError):
                 remnant.configure_cache_format(**bad)
+        for count in config.KEEP_COUNTS:
+            c = remnant.configure_cache_format("remnant", "triton", keep_count=count)
+            assert c.decode_impl == "reconstruct" and c.record_bytes == count + 72
+            assert remnant.packed_profile()["page_bytes"] == 64 * (count + 72)
+        c = remnant.configure_cache_format("remnant", "reconstruct",
+                                           layer_keep_counts=[64, 256, 448])
+        assert [c.record_bytes_for(i) for i in range(3)] == [136, 328, 520]
         import argparse
         p = argparse.ArgumentParser()
         config.add_cli_arguments(p)
@@ -194,3 +215,37 @@ def test_pool_planes_and_capacity():
     packed, native = remnant.records_fitting(hbm, "direct"), remnant.records_fitting(hbm, "native")
     assert abs(packed / 878.0e6 - 1) < 1e-3 and abs(native / 493.2e6 - 1) < 1e-3
     assert abs(packed / native - 584 / 328) < 1e-3
+
+
+def test_survivor_profile_pools():
+    """(K + 72)-byte records, 64 to a page; planes are views; a raw page tensor's
+    size names its profile; the Direct reader refuses non-256 pools."""
+    for count in config.KEEP_COUNTS:
+        pool = remnant.LatentPool(2, device="cpu", keep_count=count)
+        assert pool.page_bytes == 64 * (count + 72) and pool.record_bytes == count + 72
+        assert pool.values().shape == (2, 64, count)
+        assert pool.bitmaps().shape == (2, 64, 64) and pool.scales().shape == (2, 64, 8)
+        pool.values()[1, 3] = 5
+        pool.bitmaps()[1, 3] = 6
+        pool.scales()[1, 3] = 7
+        rec = pool.records(torch.tensor([67]))[0]
+        assert torch.equal(pool.layer()[1, 3 * (count + 72):4 * (count + 72)], rec)
+        assert torch.all(rec[:count] == 5) and torch.all(rec[count:count + 64] == 6)
+        assert torch.all(rec[count + 64:] == 7)
+        raw = torch.zeros((1, pool.page_bytes), dtype=torch.uint8)
+        assert remnant.packed._as_pool(raw, None)[1:] == (True, count)
+        assert config.packed_page_bytes(count) % 16 == 0
+    with pytest.raises(ValueError):
+        remnant.LatentPool(1, device="cpu", keep_count=512)
+    with pytest.raises(ValueError):
+        remnant.LatentPool(1, fmt="native", device="cpu", keep_count=192)
+    with pytest.raises(ValueError, match="unknown page size"):
+        remnant.packed._as_pool(torch.zeros((1, 64 * 300), dtype=torch.uint8), None)
+    q = torch.zeros((1, 1, 16, 512), dtype=torch.bfloat16)
+    bt = torch.zeros((1, 1), dtype=torch.int32)
+    idx = torch.zeros((1, 1, 4), dtype=torch.int32)
+    with pytest.raises(ValueError, match="256-survivor"):
+        remnant.remnant_sparse_decode_fwd(q, remnant.LatentPool(1, device="cpu", keep_count=192),
+                                          bt, idx)
+    hbm = 288 * 10**9
+    assert remnant.records_fitting(hbm, "direct", 64) > remnant.records_fitting(hbm, "direct")

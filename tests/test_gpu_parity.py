@@ -25,8 +25,9 @@ def banner(msg):
     print(f"[gpu-parity] {msg}", flush=True)
 
 
-def gpu_pack(x: torch.Tensor, slots: np.ndarray, pages: int, weight=None, eps=1e-6, fill=0):
-    pool = remnant.LatentPool(pages, fmt="remnant", device=DEV)
+def gpu_pack(x: torch.Tensor, slots: np.ndarray, pages: int, weight=None, eps=1e-6, fill=0,
+             keep_count=256):
+    pool = remnant.LatentPool(pages, fmt="remnant", device=DEV, keep_count=keep_count)
     pool.buffer.fill_(fill)
     w = torch.ones(512) if weight is None else torch.as_tensor(weight)
     remnant.pack_rows_fused(x.to(DEV), w.float().to(DEV), eps,
@@ -35,10 +36,11 @@ def gpu_pack(x: torch.Tensor, slots: np.ndarray, pages: int, weight=None, eps=1e
     return pool
 
 
-def oracle_pack(x: torch.Tensor, slots, pages, weight=None, eps=1e-6, fill=0):
-    pool = np.full((pages, oracle.PAGE_BYTES), fill, np.uint8)
+def oracle_pack(x: torch.Tensor, slots, pages, weight=None, eps=1e-6, fill=0, keep_count=256):
+    pool = np.full((pages, oracle.page_bytes(keep_count)), fill, np.uint8)
     w = W1 if weight is None else np.asarray(weight, np.float32)
-    oracle.pack_rows_paged(x.float().numpy(), w, eps, np.asarray(slots, np.int32), pool)
+    oracle.pack_rows_paged(x.float().numpy(), w, eps, np.asarray(slots, np.int32), pool,
+                           keep_count)
     return pool
 
 
@@ -158,6 +160,116 @@ def test_native_store_bit_exact():
     oracle.native_pack_rows_paged(x.float().numpy(), W1, 1e-6, slots, positions,
                                   torch.view_as_real(freqs).numpy(), ref)
     assert np.array_equal(pool.layer().cpu().numpy(), ref)
+
+
+# ---- survivor profiles 64..448 (count + 72 byte records) ------------------------------------
+
+KEEPS = [64, 128, 192, 256, 320, 384, 448]
+
+
+@pytest.mark.parametrize("keep_count", KEEPS)
+def test_pack_bit_exact_survivor_profiles(keep_count):
+    """Every profile, both input dtypes: random rows plus heavy integer ties,
+    shuffled slots with skipped ones, canary bytes elsewhere."""
+    banner(f"pack survivor profile {keep_count}")
+    rng = np.random.default_rng(keep_count)
+    ints = torch.from_numpy(rng.integers(-6, 7, (64, 512)).astype(np.float32))
+    x = torch.cat([syn.latents(1024, seed=40 + keep_count).float(), ints])
+    slots = rng.permutation(18 * 64)[:1088].astype(np.int32)
+    slots[::97] = -1
+    for dtype in (torch.float32, torch.bfloat16):
+        assert_pool_equal(
+            gpu_pack(x.to(dtype), slots, 18, fill=0x5A, keep_count=keep_count),
+            oracle_pack(x.to(dtype), slots, 18, fill=0x5A, keep_count=keep_count))
+
+
+@pytest.mark.parametrize("keep_count", KEEPS)
+def test_unpack_gather_bit_exact_survivor_profiles(keep_count):
+    """Reconstruct (with and without RoPE) on every profile: strided indices,
+    invalid and padded selections, canary rows past the output."""
+    banner(f"unpack_gather survivor profile {keep_count}")
+    pages = 4
+    rng = np.random.default_rng(60 + keep_count)
+    x = syn.latents(pages * 64, seed=60 + keep_count)
+    slots = rng.permutation(pages * 64).astype(np.int32)
+    pool = gpu_pack(x, slots, pages, keep_count=keep_count)
+    ref_pool = pool.layer().cpu().numpy()
+    assert np.array_equal(ref_pool, oracle_pack(x, slots, pages, keep_count=keep_count))
+    nq, nk = 3, 80
+    physical = rng.integers(-2, pages * 64 + 3, (nq, nk)).astype(np.int32)
+    raw = rng.integers(-1, 70, (nq, nk)).astype(np.int32)
+    lengths = np.array([80, 7, 0], np.int32)
+    freqs = syn.rope_freqs(4 * 64)  # raw >= 64 is beyond the table
+    wide = torch.zeros((nq, 2 * nk), dtype=torch.int32)
+    wide[:, ::2] = torch.from_numpy(physical)
+    ph_d = wide.to(DEV)[:, ::2]
+    rw_d = torch.from_numpy(raw).to(DEV)
+    len_d = torch.from_numpy(lengths).to(DEV)
+    out = torch.full((nq * nk + 3, 512), -91.0, dtype=torch.bfloat16, device=DEV)
+    remnant.unpack_gather_bf16(pool, ph_d, rw_d, len_d, freqs.to(DEV), out, fused_rope=True)
+    plain = torch.empty((nq * nk, 512), dtype=torch.bfloat16, device=DEV)
+    remnant.unpack_gather_bf16(pool, ph_d, None, len_d, None, plain)
+    torch.cuda.synchronize()
+    expect = oracle.unpack_gather(ref_pool, physical, raw, lengths,
+                                  torch.view_as_real(freqs).numpy(), keep_count=keep_count)
+    assert np.array_equal(syn.bf16_bits(out)[:nq * nk], expect)
+    assert np.all(out[nq * nk:].float().cpu().numpy() == -91)
+    expect_plain = oracle.unpack_gather(ref_pool, physical, None, lengths,
+                                        keep_count=keep_count)
+    assert np.array_equal(syn.bf16_bits(plain), expect_plain)
+
+
+def test_reconstruct_graph_replays_changed_records_indices_lengths_and_frequencies():
+    """Mirror of the reference's graph test (candidate-sglang.patch:775-865) for
+    every profile: the reader captured once in a HIP graph, then replayed after
+    the records, indices, lengths and frequencies change in place; every replay
+    matches the oracle and an eager call."""
+    g = torch.Generator().manual_seed(101)
+    weight = torch.linspace(0.5, 1.5, 512)
+    for count in KEEPS:
+        banner(f"graph replay survivor profile {count}")
+        pool = remnant.LatentPool(1, device=DEV, keep_count=count)
+        source = torch.randn(4, 512, generator=g)
+        loc = torch.arange(4, dtype=torch.int32, device=DEV)
+        remnant.pack_rows_fused(source.to(DEV), weight.to(DEV), 1e-6, loc, pool)
+        physical = torch.tensor([[0, 2, -1, 3], [3, 3, 1, 0]], dtype=torch.int32, device=DEV)
+        raw = torch.tensor([[0, 2, 1, 3], [2, 0, 1, 4]], dtype=torch.int32, device=DEV)
+        lengths = torch.tensor([4, 3], dtype=torch.int32, device=DEV)
+        angles = torch.arange(32 * 32).float().reshape(32, 32) * 0.0037
+        freqs = torch.polar(torch.ones_like(angles), angles).to(DEV)
+        output = torch.empty((8, 512), dtype=torch.bfloat16, device=DEV)
+        eager = torch.empty_like(output)
+
+        def call():
+            remnant.unpack_gather_bf16(pool, physical, raw, lengths, freqs, output,
+                                       fused_rope=True)
+
+        call()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            call()
+        torch.cuda.synchronize()
+        for iteration in range(3):
+            source = torch.randn(4, 512, generator=g)
+            remnant.pack_rows_fused(source.to(DEV), weight.to(DEV), 1e-6, loc, pool)
+            physical.copy_(physical.roll(1, dims=1))
+            raw.copy_(raw.roll(1, dims=1))
+            raw[0, 1] = -1
+            lengths.copy_(torch.tensor([4 - iteration, 2 + iteration], dtype=torch.int32))
+            phase = angles * (iteration + 2)
+            freqs.copy_(torch.polar(torch.ones_like(phase), phase))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            remnant.unpack_gather_bf16(pool, physical, raw, lengths, freqs, eager)
+            torch.cuda.synchronize()
+            expect = oracle.unpack_gather(pool.layer().cpu().numpy(), physical.cpu().numpy(),
+                                          raw.cpu().numpy(), lengths.cpu().numpy(),
+                                          torch.view_as_real(freqs.cpu()).numpy(),
+                                          keep_count=count)
+            assert np.array_equal(syn.bf16_bits(output), expect), (count, iteration)
+            assert torch.equal(output.view(torch.int16), eager.view(torch.int16))
 
 
 # ---- decode -----------------------------------------------------------------------------

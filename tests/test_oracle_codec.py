@@ -301,3 +301,105 @@ def test_unpack_gather_validity_rules():
             assert np.array_equal(out[row], ref[0])
     zero_rows = [row for row in range(8) if not out[row].any()]
     assert zero_rows == [2, 5, 7]
+
+
+# ---- survivor profiles 64..448 (count + 72 byte records) -----------------------
+
+def ranking_rule(x: np.ndarray, retained: int) -> np.ndarray:
+    """evaluate.py:65-91 with one 512-group: prune topk(|x|, 512 - retained,
+    largest=False); budgets RETENTION_COUNTS = 64..448 (losses.py:17)."""
+    t = torch.from_numpy(x).abs()
+    mask = torch.ones_like(t, dtype=torch.bool)
+    mask.scatter_(-1, t.topk(512 - retained, dim=-1, largest=False).indices, False)
+    return mask.numpy()
+
+
+@pytest.mark.parametrize("keep_count", oracle.KEEP_COUNTS)
+def test_selection_any_survivor_count(keep_count):
+    """Untied rows agree with the reference's ranking rule; tied rows follow the
+    rank rule (#{greater} + #{equal, lower coordinate} < K) by brute force."""
+    rng = np.random.default_rng(30 + keep_count)
+    x = rng.standard_normal((48, 512)).astype(np.float32)
+    x = x[[len(np.unique(np.abs(r))) == 512 for r in x]]
+    assert len(x) > 20
+    assert np.array_equal(oracle.select_keep(x, keep_count), ranking_rule(x, keep_count))
+    t = rng.integers(-6, 7, (6, 512)).astype(np.float32)
+    keep = oracle.select_keep(t, keep_count)
+    a = np.abs(t)
+    bigger = (a[:, None, :] > a[:, :, None]).sum(2)          # [row, c]: #{j : |x_j| > |x_c|}
+    lower = np.arange(512)[None, :] < np.arange(512)[:, None]  # [c, j]: j < c
+    tied_before = ((a[:, None, :] == a[:, :, None]) & lower).sum(2)
+    assert np.array_equal(keep, bigger + tied_before < keep_count)
+    assert (keep.sum(1) == keep_count).all()
+
+
+@pytest.mark.parametrize("keep_count", oracle.KEEP_COUNTS)
+def test_packed_record_closed_form_any_survivor_count(keep_count):
+    """K survivors at coordinates c % 8 < K / 64, weight 2^tile: every byte of
+    the (K + 72)-byte record follows from the math (codes K/8 per group, bitmap
+    bytes with their top K/64 bits set, scale ceil(log2(n / 448)) + 127)."""
+    eps, per = 1e-6, keep_count // 64
+    x = (np.arange(512) % 8 < per).astype(np.float32)
+    weight = np.repeat(np.array([2.0**t for t in range(8)], np.float32), 64)
+    data, scales, normed, keep = oracle.pack_rows(x[None], weight, eps, keep_count)
+    assert data.shape == (1, keep_count + 64)
+    assert np.array_equal(keep[0], x != 0)
+    assert np.all(data[0, keep_count:] == (0xFF << (8 - per)) & 0xFF)
+    for tile in range(8):
+        n = float(torch.tensor((2.0**tile) / math.sqrt(keep_count / 512 + eps)).bfloat16())
+        e = math.ceil(math.log2(n / 448))
+        assert scales[0, tile] == e + 127
+        code = int(torch.tensor(n / 2.0**e).to(torch.float8_e4m3fn).view(torch.uint8))
+        assert np.all(data[0, tile * 8 * per:(tile + 1) * 8 * per] == code)
+    dec = oracle.bf16_to_f32(oracle.unpack_row(data[0], scales[0], keep_count))
+    assert np.all(dec[x == 0] == 0) and np.all(dec[x != 0] > 0)
+
+
+@pytest.mark.parametrize("keep_count", [64, 192, 448])
+def test_pack_unpack_roundtrip_any_survivor_count(keep_count):
+    """unpack(pack(x)) equals the dense simulation of the same mask; the paged
+    pool of (K + 72)-byte records holds the same bytes as the row packer."""
+    x = oracle.synthetic_latents(96, seed=7 + keep_count)
+    data, scales, normed, keep = oracle.pack_rows(x, ONES, 1e-6, keep_count)
+    dec = oracle.unpack_rows(data, scales, keep_count)
+    assert np.array_equal(dec, oracle.simulate_rows(x, keep, ONES, 1e-6))
+    assert np.all(np.unpackbits(data[:, keep_count:], axis=1).sum(1) == keep_count)
+    slots = np.random.default_rng(9).permutation(128)[:96].astype(np.int32)
+    pool = np.zeros((2, oracle.page_bytes(keep_count)), np.uint8)
+    oracle.pack_rows_paged(x, ONES, 1e-6, slots, pool, keep_count)
+    recs = pool.reshape(128, oracle.record_bytes(keep_count))
+    assert np.array_equal(recs[slots], np.concatenate([data, scales], axis=1))
+    lengths = np.array([96], np.int32)
+    got = oracle.unpack_gather(pool, slots[None], None, lengths, keep_count=keep_count)
+    assert np.array_equal(got, dec)
+
+
+@pytest.mark.parametrize("keep_count", [192, 448])
+def test_rotation_reaches_pruned_partner_lanes_any_survivor_count(keep_count):
+    """candidate-sglang.patch:707-736 (parametrized over 192 and 256 there):
+    survivors 0..K-3 plus 448 and 451; the rotation fills pruned 449 and 450."""
+    latent = np.zeros((2, 512), np.float32)
+    latent[:, : keep_count - 2] = 2
+    latent[:, 448] = 3
+    latent[:, 451] = -3
+    keep = oracle.select_keep(latent, keep_count)
+    assert np.array_equal(keep, latent != 0)
+    pool = np.zeros((1, oracle.page_bytes(keep_count)), np.uint8)
+    oracle.pack_rows_paged(latent, ONES, 1e-6, np.array([0, 1], np.int32), pool, keep_count)
+    angles = torch.linspace(0.2, 1.1, 16 * 32).reshape(16, 32)
+    freqs = torch.polar(torch.ones_like(angles), angles)
+    out = oracle.unpack_gather(pool, np.array([[1, 1]]), np.array([[0, 2]]), np.array([2]),
+                               torch.view_as_real(freqs).numpy(), keep_count=keep_count)
+    dec = oracle.unpack_gather(pool, np.array([[1, 1]]), None, np.array([2]),
+                               keep_count=keep_count)
+    expected = rotate_torch(dec, freqs[[0, 8]])
+    assert np.all(oracle.bf16_to_f32(expected[:, [449, 450]]) != 0)
+    assert np.abs(out.astype(np.int32) - expected.astype(np.int32)).max() <= 1
+
+
+def test_survivor_count_outside_profiles_is_rejected():
+    """512 survivors (and non-multiples of 64) are not profiles
+    (docs/agents/numerical-and-validation.md:11-13)."""
+    for bad in (0, 32, 200, 512):
+        with pytest.raises(ValueError):
+            oracle.select_keep(np.zeros((1, 512), np.float32), bad)
