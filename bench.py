@@ -62,6 +62,8 @@ def parse():
     p.add_argument("--quick", action="store_true", help="skip decode, capacity and CPU legs")
     p.add_argument("--no-capacity", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-reference-shapes", action="store_true",
+                   help="skip the reference's H64/H128 decode shapes")
     p.add_argument("--cpu-sample", type=int, default=196608)
     p.add_argument("--keep-count", type=int, default=256,
                    help="survivor profile of the bulk leg (64..448, step 64)")
@@ -134,8 +136,10 @@ def bulk(torch, remnant, args):
                 recon_ms=recon_ms, rope_ms=rope_ms)
 
 
-def build_decode(torch, remnant, contexts, q_len, topk, packed, seed, pool_pages=None):
-    """Pack the contexts' records into a (possibly much larger) paged pool."""
+def build_decode(torch, remnant, contexts, q_len, topk, packed, seed, pool_pages=None, heads=16,
+                 swa=0):
+    """Pack the contexts' records into a (possibly much larger) paged pool; with
+    swa > 0 every token also gets `swa` window rows of its own in a Native pool."""
     syn = remnant.synthetic
     dev = "cuda"
     table, pages = syn.paged_requests(contexts, seed, pool_pages)
@@ -157,23 +161,34 @@ def build_decode(torch, remnant, contexts, q_len, topk, packed, seed, pool_pages
             else:
                 remnant.native_store_rows(x, w, 1e-6, slot, r.to(torch.int32), freqs, pool)
     idx, lens = syn.topk_indices(contexts, q_len, topk, seed + 1)
-    q = (torch.randn(len(contexts), q_len, 16, 512, device=dev, generator=g) * 0.5).to(torch.bfloat16)
-    sink = torch.randn(16, device=dev, generator=g)
-    return dict(pool=pool, table=tab, idx=torch.from_numpy(idx).to(dev),
-                lens=torch.from_numpy(lens).to(dev),
-                seqlens=torch.tensor(contexts, dtype=torch.int32, device=dev), q=q, sink=sink,
-                freqs=freqs, packed=packed, valid=int(lens.sum()))
+    q = (torch.randn(len(contexts), q_len, heads, 512, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    sink = torch.randn(heads, device=dev, generator=g)
+    c = dict(pool=pool, table=tab, idx=torch.from_numpy(idx).to(dev),
+             lens=torch.from_numpy(lens).to(dev),
+             seqlens=torch.tensor(contexts, dtype=torch.int32, device=dev), q=q, sink=sink,
+             freqs=freqs, packed=packed, valid=int(lens.sum()), swa=swa)
+    if swa:
+        rows = len(contexts) * q_len * swa
+        spool = remnant.LatentPool((rows + 63) // 64, fmt="native", device=dev)
+        slot = torch.arange(rows, dtype=torch.int32, device=dev)
+        x = (torch.randn(rows, 512, device=dev, generator=g) * sigma).to(torch.bfloat16)
+        remnant.native_store_rows(x, w, 1e-6, slot, slot % max(contexts), freqs, spool)
+        c["swa_pool"] = spool
+        c["swa_idx"] = slot.view(len(contexts), q_len, swa)
+    return c
 
 
 def time_decode(torch, remnant, c, reps=10, warm=5, samples=20):
     """Median µs per decode call, from HIP-graph replays of `reps` calls."""
     tokens, heads = c["q"].shape[0] * c["q"].shape[1], c["q"].shape[2]
-    _, need = remnant.get_decode_metadata(tokens, heads, c["idx"].shape[-1])
+    _, need = remnant.get_decode_metadata(tokens, heads, c["idx"].shape[-1], c["swa"])
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
     out = torch.empty_like(c["q"])
     lse = torch.empty(c["q"].shape[:3], dtype=torch.float32, device="cuda")
     kw = dict(seqlens=c["seqlens"], topk_length=c["lens"], sink=c["sink"], out=out, lse=lse,
               workspace=ws)
+    if c["swa"]:
+        kw.update(swa_pool=c["swa_pool"], swa_indices=c["swa_idx"])
 
     def call():
         if c["packed"]:
@@ -211,7 +226,8 @@ def decode_bytes(c, rope_table: bool):
     rec = 328 if c["packed"] else 584
     per = rec + (256 if (rope_table and c["packed"]) else 0)
     tokens, heads = c["q"].shape[0] * c["q"].shape[1], c["q"].shape[2]
-    return c["valid"] * per + 2 * tokens * heads * 512 * 2 + c["idx"].numel() * 4
+    return (c["valid"] * per + 2 * tokens * heads * 512 * 2 + c["idx"].numel() * 4
+            + tokens * c["swa"] * (584 + 4))
 
 
 def decode_leg(torch, remnant, args):
@@ -244,6 +260,43 @@ def decode_leg(torch, remnant, args):
             del c
             torch.cuda.empty_cache()
         entry["packed_over_native_time"] = entry["direct_packed"]["us_per_step"] / entry["native"]["us_per_step"]
+        res[name] = entry
+    if not args.no_reference_shapes:
+        res["reference_shapes"] = reference_shapes_leg(torch, remnant)
+    return res
+
+
+# The reference's published decode cases (H100, complete operation including
+# combine, CUDA-graph replays; dsv4-flash-decode-store timing.json / README.md):
+# heads, batch, valid top-k of 512, 64 window rows, one query token.
+REFERENCE_DECODE_US = {  # case: (Native µs, Direct µs) on H100
+    "h64_b8_k512": (14.874, 19.307), "h64_b8_k317": (13.307, 17.206),
+    "h64_b16_k512": (18.054, 23.292), "h64_b16_k317": (15.487, 19.644),
+    "h128_b8_k512": (16.710, 19.791), "h128_b8_k317": (14.971, 17.385),
+    "h128_b16_k512": (20.945, 25.824), "h128_b16_k317": (17.968, 21.967),
+}
+
+
+def reference_shapes_leg(torch, remnant):
+    """The same eight shapes on this GPU: Direct (Packed) and Native decodes with
+    64 window rows per token, 512-entry top-k lists (317 valid in the k317
+    cases) over 4096-record contexts, timed from HIP-graph replays."""
+    res = {}
+    for name, (ref_native, ref_direct) in REFERENCE_DECODE_US.items():
+        heads, batch, valid = (int(v[1:]) for v in name.split("_"))
+        entry = {"heads": heads, "batch": batch, "topk": 512, "topk_length": valid,
+                 "swa_rows": 64, "reference_h100_us": {"native": ref_native, "direct": ref_direct}}
+        for packed in (True, False):
+            log(f"decode reference shape {name} packed={packed}")
+            c = build_decode(torch, remnant, [4096] * batch, 1, 512, packed, 17, heads=heads,
+                             swa=64)
+            c["lens"].fill_(valid)
+            c["valid"] = batch * valid
+            us, _, _ = time_decode(torch, remnant, c)
+            entry["direct_packed_us" if packed else "native_us"] = us
+            del c
+            torch.cuda.empty_cache()
+        entry["packed_over_native_time"] = entry["direct_packed_us"] / entry["native_us"]
         res[name] = entry
     return res
 

@@ -78,11 +78,13 @@ struct DecodeArgs {
   int64_t q_len;
   int64_t heads;
   int chunk;       // records per split (multiple of 32, <= kPcMaxChunk)
-  int splits;
+  int splits;      // splits of this list (workgroups along x)
+  int ws_splits;   // partial slots per row in the workspace; 0: finalise in place
+  int ws_base;     // slot of this list's split 0
   uint16_t* out;
   float* lse;
-  float* ws_o;     // [tokens, splits, heads, 512]
-  float* ws_lse;   // [tokens, splits, heads]
+  float* ws_o;     // [tokens, ws_splits, heads, 512]
+  float* ws_lse;   // [tokens, ws_splits, heads]
 };
 
 // Two E4M3 codes (bytes 0-1, or 2-3 with kHi) times scale -> two BF16 (exact).
@@ -168,6 +170,26 @@ struct PcGeo {
   static constexpr int kDepth = 4;  // copy ring buffers (the step loop is unrolled by 4)
 };
 
+// Shared memory of one workgroup. The kernels declare one byte array of the
+// larger format's size and view it as the format they run, so a kernel that
+// runs either format per workgroup needs no more LDS than the larger one.
+template <bool kPacked>
+struct PcShared {
+  using G = PcGeo<kPacked>;
+  uint8_t raw[kPcProducers][G::kDepth][G::kBuf];  // copy ring (LDS address 0)
+  uint16_t ktile[kPcRing][kT * kPcKPitch];
+  // per record slot of the split: pool row address, or (Q address | 1) for an
+  // invalid record or a slot past the end (a readable stand-in source, odd so
+  // that bit 0 marks it); Packed: RoPE row address (row 0 of the table for an
+  // invalid record, Q without a table)
+  uint64_t row_tab[kPcMaxChunk];
+  uint64_t aux_tab[kPacked ? kPcMaxChunk : 1];
+  uint64_t sel_tab[kPacked ? 256 : 1];
+  float mrg[kPcConsumers][2][16];  // consumers' (m_ref, l) per head
+};
+constexpr size_t kPcSmemBytes = sizeof(PcShared<true>) > sizeof(PcShared<false>)
+                                    ? sizeof(PcShared<true>) : sizeof(PcShared<false>);
+
 // Max of x over lanes col, col + 16, col + 32, col + 48 (col = lane % 16).
 __device__ __forceinline__ float max_over_rows(float x) {
   const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
@@ -178,24 +200,22 @@ __device__ __forceinline__ float max_over_rows(float x) {
   return fmaxf(u2f(r[0]), u2f(r[1]));
 }
 
+// One workgroup's share: split `split` of list `a` (a C4 top-k list through
+// the block table, or with a.block_table == nullptr a list of pool slots).
 template <bool kPacked>
-__device__ __forceinline__ void decode_pc(const DecodeArgs& a) {
+__device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>* sm,
+                                          const int split) {
   using G = PcGeo<kPacked>;
-  __shared__ __attribute__((aligned(16))) uint16_t ktile[kPcRing][kT * kPcKPitch];
-  __shared__ __attribute__((aligned(16))) uint8_t raw[kPcProducers][G::kDepth][G::kBuf];
-  __shared__ __attribute__((aligned(16))) uint64_t sel_tab[kPacked ? 256 : 1];
-  // per record slot of the split: pool row address, or (Q address | 1) for an
-  // invalid record or a slot past the end (a readable stand-in source, odd so
-  // that bit 0 marks it); Packed: RoPE row address (row 0 of the table for an
-  // invalid record, Q without a table)
-  __shared__ uint64_t row_tab[kPcMaxChunk];
-  __shared__ uint64_t aux_tab[kPacked ? kPcMaxChunk : 1];
-  __shared__ float mrg[kPcConsumers][2][16];  // consumers' (m_ref, l) per head
+  auto& ktile = sm->ktile;
+  auto& raw = sm->raw;
+  auto& sel_tab = sm->sel_tab;
+  auto& row_tab = sm->row_tab;
+  auto& aux_tab = sm->aux_tab;
+  auto& mrg = sm->mrg;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = uniform(tid >> 6);
-  const int split = blockIdx.x;
   const int64_t t = blockIdx.y;
   const int64_t head0 = (int64_t)blockIdx.z * 16;
   const int64_t b = t / a.q_len;
@@ -239,8 +259,13 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a) {
     int64_t r = 0, page = 0;
     if (i < n) {
       r = a.indices[t * a.topk + k0 + i];
-      ok = r >= 0 && r < seqlen && (r >> 6) < a.max_blocks;
-      page = ok ? a.block_table[b * a.bt_stride + (r >> 6)] : -1;
+      if (a.block_table) {  // logical record of request b
+        ok = r >= 0 && r < seqlen && (r >> 6) < a.max_blocks;
+        page = ok ? a.block_table[b * a.bt_stride + (r >> 6)] : -1;
+      } else {  // pool slot
+        ok = r >= 0;
+        page = r >> 6;
+      }
       ok = ok && page >= 0 && page < a.pool_pages;
       if (kPacked && a.freqs) ok = ok && r * 4 < a.freq_rows;
     }
@@ -611,7 +636,7 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a) {
   l_run += __shfl_xor(l_run, 32, 64);  // sum of the weights of head col against m_ref
   const float mm = m_ref;
   float factor_h, lse_h;
-  if (a.splits == 1) {
+  if (a.ws_splits == 0) {
     const float sink2 = a.sink ? a.sink[head0 + col] * kLog2e : -INFINITY;
     const float mz = fmaxf(mm, sink2);
     factor_h = 0.0f;
@@ -626,19 +651,20 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a) {
   } else {
     factor_h = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     lse_h = l_run > 0.0f ? mm + log2f(l_run) : -INFINITY;
-    if (half == 0 && lane < 16) a.ws_lse[(t * a.splits + split) * a.heads + head0 + col] = lse_h;
+    if (half == 0 && lane < 16)
+      a.ws_lse[(t * a.ws_splits + a.ws_base + split) * a.heads + head0 + col] = lse_h;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int h = 4 * g + i;
     const float f = __shfl(factor_h, h, 64);
-    if (a.splits == 1) {
+    if (a.ws_splits == 0) {
       uint16_t* orow = a.out + (t * a.heads + head0 + h) * kHeadDim + 256 * half + col;
 #pragma unroll
       for (int nt = 0; nt < 16; ++nt)
         orow[16 * nt] = __builtin_bit_cast(uint16_t, (__bf16)(o[nt][i] * f));
     } else {
-      float* orow = a.ws_o + ((t * a.splits + split) * a.heads + head0 + h) * kHeadDim +
+      float* orow = a.ws_o + ((t * a.ws_splits + a.ws_base + split) * a.heads + head0 + h) * kHeadDim +
                     256 * half + col;
 #pragma unroll
       for (int nt = 0; nt < 16; ++nt) orow[16 * nt] = o[nt][i] * f;
@@ -647,10 +673,30 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a) {
 }
 
 __global__ __launch_bounds__(kPcThreads) void packed_decode_pc_kernel(DecodeArgs a) {
-  decode_pc<true>(a);
+  __shared__ __attribute__((aligned(16))) uint8_t smem[sizeof(PcShared<true>)];
+  decode_pc<true>(a, reinterpret_cast<PcShared<true>*>(smem), blockIdx.x);
 }
 __global__ __launch_bounds__(kPcThreads) void native_decode_pc_kernel(DecodeArgs a) {
-  decode_pc<false>(a);
+  __shared__ __attribute__((aligned(16))) uint8_t smem[sizeof(PcShared<false>)];
+  decode_pc<false>(a, reinterpret_cast<PcShared<false>*>(smem), blockIdx.x);
+}
+// C4 list and window rows in one launch: workgroups x < c4.splits take a C4
+// split, the last column the window rows (Native records).
+template <bool kPacked>
+__device__ __forceinline__ void decode_joint(const DecodeArgs& c4, const DecodeArgs& swa) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kPcSmemBytes];
+  if ((int)blockIdx.x < c4.splits)
+    decode_pc<kPacked>(c4, reinterpret_cast<PcShared<kPacked>*>(smem), blockIdx.x);
+  else
+    decode_pc<false>(swa, reinterpret_cast<PcShared<false>*>(smem), 0);
+}
+__global__ __launch_bounds__(kPcThreads) void packed_swa_decode_pc_kernel(DecodeArgs c4,
+                                                                         DecodeArgs swa) {
+  decode_joint<true>(c4, swa);
+}
+__global__ __launch_bounds__(kPcThreads) void native_swa_decode_pc_kernel(DecodeArgs c4,
+                                                                         DecodeArgs swa) {
+  decode_joint<false>(c4, swa);
 }
 
 // Merge split partials with the sink, for many rows. One workgroup (4 waves)
@@ -778,18 +824,22 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 struct Plan {
   int splits;
   int chunk;
-  size_t bytes;
 };
 
 // Split plan: about one workgroup per CU (256 CUs), whole 32-record stages per
-// split, at most kPcMaxChunk records per split.
-Plan plan_pc(int64_t tokens, int64_t heads, int64_t topk) {
+// split, at most kPcMaxChunk records per split and max_splits splits (the
+// combine merges at most kMaxSplits partial slots per row, the window rows'
+// slot included).
+Plan plan_pc(int64_t tokens, int64_t heads, int64_t topk, int64_t max_splits = kMaxSplits,
+             bool window = false) {
   const int64_t base = tokens * (heads / 16);
   const int64_t stages = (topk + kPcStage - 1) / kPcStage;
   int64_t splits = base > 0 ? (256 + base - 1) / base : 1;
+  // the window rows' workgroups (one per token and head block) share the round
+  if (window && base > 0) splits = 256 / base - 1;
   const int64_t min_splits = (topk + kPcMaxChunk - 1) / kPcMaxChunk;
   if (splits > stages) splits = stages;
-  if (splits > kMaxSplits) splits = kMaxSplits;
+  if (splits > max_splits) splits = max_splits;
   if (splits < min_splits) splits = min_splits;
   if (splits < 1) splits = 1;
   int64_t chunk_stages = (stages + splits - 1) / splits;
@@ -799,36 +849,58 @@ Plan plan_pc(int64_t tokens, int64_t heads, int64_t topk) {
   Plan p;
   p.splits = (int)splits;
   p.chunk = (int)(chunk_stages * kPcStage);
-  p.bytes = splits > 1 ? (size_t)(tokens * splits * heads) * (kHeadDim + 1) * sizeof(float) : 0;
   return p;
 }
 
 bool aligned(const void* p, uintptr_t al) { return ((uintptr_t)p & (al - 1)) == 0; }
+
+// Sliding-window rows attended jointly with the C4 list: slots of a Native
+// pool (64-record pages, tail stored rotated), per token.
+struct Swa {
+  const uint8_t* pool = nullptr;
+  int64_t pool_pages = 0;
+  const int32_t* indices = nullptr;  // [tokens, topk] pool slots (-1 = padding)
+  int64_t topk = 0;
+  const int32_t* length = nullptr;   // [tokens] valid entries (NULL = topk)
+};
+
+// Workspace slots per row: the C4 splits, plus one for the window rows.
+int64_t ws_slots(const Plan& p, const Swa& w) { return p.splits + (w.topk > 0 ? 1 : 0); }
+// C4 splits available next to the window rows' slot.
+int64_t c4_max_splits(const Swa& w) { return kMaxSplits - (w.topk > 0 ? 1 : 0); }
+size_t ws_bytes(int64_t tokens, int64_t heads, int64_t slots) {
+  return slots > 1 ? (size_t)(tokens * slots * heads) * (kHeadDim + 1) * sizeof(float) : 0;
+}
 
 template <bool kPacked>
 int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads,
                   const uint8_t* pool, int64_t pool_pages, const int32_t* block_table,
                   int64_t bt_stride, int64_t max_blocks, const int32_t* seqlens,
                   const int32_t* indices, int64_t topk, const int32_t* topk_length,
-                  const float* sink, const float* freqs, int64_t freq_rows, float scale,
-                  uint16_t* out, float* lse, void* workspace, size_t workspace_bytes,
-                  void* stream) {
-  if (batch < 0 || q_len < 0 || topk < 0 || pool_pages < 0 || max_blocks < 0 || freq_rows < 0)
+                  const Swa& w, const float* sink, const float* freqs, int64_t freq_rows,
+                  float scale, uint16_t* out, float* lse, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  if (batch < 0 || q_len < 0 || topk < 0 || pool_pages < 0 || max_blocks < 0 || freq_rows < 0 ||
+      w.topk < 0 || w.pool_pages < 0)
     return RM_ERR_SHAPE;
   const int64_t tokens = batch * q_len;
   if (tokens == 0 || heads == 0) return RM_OK;
   if (heads < 0 || heads % 16 || heads > 1024 || bt_stride < max_blocks) return RM_ERR_SHAPE;
-  if (topk > (int64_t)kPcMaxChunk * kMaxSplits) return RM_ERR_SHAPE;
-  if (pool_pages > ((int64_t)1 << 25)) return RM_ERR_SHAPE;  // slots fit in int32
-  if (!q || !out || !lse || (topk > 0 && (!indices || !pool || !block_table)))
+  if (topk > (int64_t)kPcMaxChunk * c4_max_splits(w) || w.topk > kPcMaxChunk) return RM_ERR_SHAPE;
+  if (pool_pages > ((int64_t)1 << 25) || w.pool_pages > ((int64_t)1 << 25))
+    return RM_ERR_SHAPE;  // slots fit in int32
+  if (!q || !out || !lse || (topk > 0 && (!indices || !pool || !block_table)) ||
+      (w.topk > 0 && (!w.indices || !w.pool)))
     return RM_ERR_NULL;
   if (!aligned(q, 16) || !aligned(out, 16) || (pool && !aligned(pool, 16)) ||
-      (freqs && !aligned(freqs, 16)))
+      (w.pool && !aligned(w.pool, 16)) || (freqs && !aligned(freqs, 16)))
     return RM_ERR_ALIGN;
   if (tokens > 65535) return RM_ERR_SHAPE;
-  const Plan plan = plan_pc(tokens, heads, topk);
-  if (plan.bytes > 0 && (!workspace || workspace_bytes < plan.bytes)) return RM_ERR_WORKSPACE;
-  if (plan.bytes > 0 && !aligned(workspace, 16)) return RM_ERR_ALIGN;
+  const Plan plan = plan_pc(tokens, heads, topk, c4_max_splits(w), w.topk > 0);
+  const int64_t slots = ws_slots(plan, w);
+  const size_t bytes = ws_bytes(tokens, heads, slots);
+  if (bytes > 0 && (!workspace || workspace_bytes < bytes)) return RM_ERR_WORKSPACE;
+  if (bytes > 0 && !aligned(workspace, 16)) return RM_ERR_ALIGN;
   DecodeArgs a;
   a.q = q;
   a.pool = pool;
@@ -848,24 +920,45 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   a.heads = heads;
   a.chunk = plan.chunk;
   a.splits = plan.splits;
+  a.ws_splits = slots > 1 ? (int)slots : 0;
+  a.ws_base = 0;
   a.out = out;
   a.lse = lse;
   a.ws_o = (float*)workspace;
-  a.ws_lse = plan.bytes ? (float*)workspace + (size_t)tokens * plan.splits * heads * kHeadDim
-                        : nullptr;
+  a.ws_lse = bytes ? (float*)workspace + (size_t)tokens * slots * heads * kHeadDim : nullptr;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(kPacked ? packed_decode_pc_kernel : native_decode_pc_kernel,
-                     dim3((unsigned)plan.splits, (unsigned)tokens, (unsigned)(heads / 16)),
-                     dim3(kPcThreads), 0, s, a);
+  if (w.topk > 0) {
+    // the window rows are one more split, read by the Native path of the same launch
+    DecodeArgs b = a;
+    b.pool = w.pool;
+    b.pool_pages = w.pool_pages;
+    b.block_table = nullptr;  // entries are pool slots
+    b.seqlens = nullptr;
+    b.indices = w.indices;
+    b.topk = w.topk;
+    b.topk_length = w.length;
+    b.freqs = nullptr;
+    b.freq_rows = 0;
+    b.chunk = kPcMaxChunk;
+    b.splits = 1;
+    b.ws_base = plan.splits;
+    hipLaunchKernelGGL(kPacked ? packed_swa_decode_pc_kernel : native_swa_decode_pc_kernel,
+                       dim3((unsigned)slots, (unsigned)tokens, (unsigned)(heads / 16)),
+                       dim3(kPcThreads), 0, s, a, b);
+  } else {
+    hipLaunchKernelGGL(kPacked ? packed_decode_pc_kernel : native_decode_pc_kernel,
+                       dim3((unsigned)plan.splits, (unsigned)tokens, (unsigned)(heads / 16)),
+                       dim3(kPcThreads), 0, s, a);
+  }
   if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
-  if (plan.splits > 1) {
+  if (slots > 1) {
     const int64_t rows = tokens * heads;
     if (rows < 256)  // too few rows to fill the GPU: one workgroup per 64 coordinates
       hipLaunchKernelGGL(combine_kernel, dim3((unsigned)(rows * kCombineSlices)), dim3(256), 0, s,
-                         a.ws_o, a.ws_lse, sink, plan.splits, heads, out, lse);
+                         a.ws_o, a.ws_lse, sink, (int)slots, heads, out, lse);
     else
       hipLaunchKernelGGL(combine_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, a.ws_o,
-                         a.ws_lse, sink, plan.splits, heads, out, lse);
+                         a.ws_lse, sink, (int)slots, heads, out, lse);
     if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   }
   return RM_OK;
@@ -875,12 +968,21 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
 
 extern "C" int rm_sparse_decode_workspace(int64_t tokens, int64_t heads, int64_t topk,
                                           int32_t* num_splits, size_t* workspace_bytes) {
-  if (tokens < 0 || heads < 0 || heads % 16 || topk < 0 ||
-      topk > (int64_t)kPcMaxChunk * kMaxSplits)
+  return rm_sparse_decode_workspace_swa(tokens, heads, topk, 0, num_splits, workspace_bytes);
+}
+
+extern "C" int rm_sparse_decode_workspace_swa(int64_t tokens, int64_t heads, int64_t topk,
+                                              int64_t swa_topk, int32_t* num_splits,
+                                              size_t* workspace_bytes) {
+  Swa w;
+  w.topk = swa_topk;
+  if (tokens < 0 || heads < 0 || heads % 16 || topk < 0 || swa_topk < 0 ||
+      swa_topk > kPcMaxChunk || topk > (int64_t)kPcMaxChunk * c4_max_splits(w))
     return RM_ERR_SHAPE;
-  const Plan p = plan_pc(tokens, heads, topk);
-  if (num_splits) *num_splits = p.splits;
-  if (workspace_bytes) *workspace_bytes = p.bytes;
+  const Plan p = plan_pc(tokens, heads, topk, c4_max_splits(w), w.topk > 0);
+  const int64_t slots = ws_slots(p, w);
+  if (num_splits) *num_splits = (int32_t)slots;
+  if (workspace_bytes) *workspace_bytes = ws_bytes(tokens, heads, slots);
   return RM_OK;
 }
 
@@ -893,7 +995,27 @@ extern "C" int rm_remnant_sparse_decode_fwd(
     void* stream) {
   return launch_decode<true>(q, batch, q_len, heads, pool, pool_pages, block_table,
                              block_table_stride, max_blocks, seqlens, indices, topk, topk_length,
-                             sink, freqs, freq_rows, softmax_scale, out, lse, workspace,
+                             Swa(), sink, freqs, freq_rows, softmax_scale, out, lse, workspace,
+                             workspace_bytes, stream);
+}
+
+extern "C" int rm_remnant_sparse_decode_swa_fwd(
+    const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads, const uint8_t* pool,
+    int64_t pool_pages, const int32_t* block_table, int64_t block_table_stride,
+    int64_t max_blocks, const int32_t* seqlens, const int32_t* indices, int64_t topk,
+    const int32_t* topk_length, const uint8_t* swa_pool, int64_t swa_pool_pages,
+    const int32_t* swa_indices, int64_t swa_topk, const int32_t* swa_length, const float* sink,
+    const float* freqs, int64_t freq_rows, float softmax_scale, uint16_t* out, float* lse,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  Swa w;
+  w.pool = swa_pool;
+  w.pool_pages = swa_pool_pages;
+  w.indices = swa_indices;
+  w.topk = swa_topk;
+  w.length = swa_length;
+  return launch_decode<true>(q, batch, q_len, heads, pool, pool_pages, block_table,
+                             block_table_stride, max_blocks, seqlens, indices, topk, topk_length,
+                             w, sink, freqs, freq_rows, softmax_scale, out, lse, workspace,
                              workspace_bytes, stream);
 }
 
@@ -905,8 +1027,28 @@ extern "C" int rm_native_sparse_decode_fwd(
     float* lse, void* workspace, size_t workspace_bytes, void* stream) {
   return launch_decode<false>(q, batch, q_len, heads, pool, pool_pages, block_table,
                               block_table_stride, max_blocks, seqlens, indices, topk,
-                              topk_length, sink, nullptr, 0, softmax_scale, out, lse, workspace,
-                              workspace_bytes, stream);
+                              topk_length, Swa(), sink, nullptr, 0, softmax_scale, out, lse,
+                              workspace, workspace_bytes, stream);
+}
+
+extern "C" int rm_native_sparse_decode_swa_fwd(
+    const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads, const uint8_t* pool,
+    int64_t pool_pages, const int32_t* block_table, int64_t block_table_stride,
+    int64_t max_blocks, const int32_t* seqlens, const int32_t* indices, int64_t topk,
+    const int32_t* topk_length, const uint8_t* swa_pool, int64_t swa_pool_pages,
+    const int32_t* swa_indices, int64_t swa_topk, const int32_t* swa_length, const float* sink,
+    float softmax_scale, uint16_t* out, float* lse, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  Swa w;
+  w.pool = swa_pool;
+  w.pool_pages = swa_pool_pages;
+  w.indices = swa_indices;
+  w.topk = swa_topk;
+  w.length = swa_length;
+  return launch_decode<false>(q, batch, q_len, heads, pool, pool_pages, block_table,
+                              block_table_stride, max_blocks, seqlens, indices, topk,
+                              topk_length, w, sink, nullptr, 0, softmax_scale, out, lse,
+                              workspace, workspace_bytes, stream);
 }
 
 extern "C" int rm_version(void) { return 300; }

@@ -44,6 +44,16 @@ SIGNATURES = {
     "rm_native_sparse_decode_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64,
                                            _vp, _vp, _i64, _vp, _vp, _f32, _vp, _vp, _vp, _sz,
                                            _vp]),
+    "rm_sparse_decode_workspace_swa": (_i32, [_i64, _i64, _i64, _i64,
+                                              ctypes.POINTER(ctypes.c_int32),
+                                              ctypes.POINTER(ctypes.c_size_t)]),
+    "rm_remnant_sparse_decode_swa_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
+                                                _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64,
+                                                _vp, _vp, _vp, _i64, _f32, _vp, _vp, _vp, _sz,
+                                                _vp]),
+    "rm_native_sparse_decode_swa_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
+                                               _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64,
+                                               _vp, _vp, _f32, _vp, _vp, _vp, _sz, _vp]),
 }
 
 _lib = None

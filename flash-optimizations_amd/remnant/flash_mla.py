@@ -7,6 +7,13 @@ metadata step that plans split-KV partitions. Output and LSE follow the
 reference's decode contract (output/LSE checked at atol=rtol=0.02,
 docs/report.md:20): out = softmax([logits, sink]) over the top-k rows with the
 sink column dropped, V = K, lse = natural log of the full normaliser.
+
+The sliding-window (SWA) rows a DeepSeek-V4 decode also attends (decode-store
+timing.json ``swa_length: 64``; joint softmax over cat(swa, C4 rows) plus the
+sink, training/losses.py:393-398) are passed as ``swa_pool`` (a Native pool:
+584-byte records, tail stored rotated) with per-token pool slots
+``swa_indices`` [B, Sq, W] (W <= 512, -1 = padding) and optional valid counts
+``swa_lengths`` [B * Sq]. They are read in the same launch as the C4 list.
 """
 
 from __future__ import annotations
@@ -20,18 +27,43 @@ from . import _lib, config
 from .packed import _as_pool, _check_cuda, _stream
 
 
-def get_decode_metadata(tokens: int, heads: int, topk: int) -> tuple[int, int]:
-    """(num_splits, workspace_bytes) for a decode of ``tokens`` query tokens."""
+def get_decode_metadata(tokens: int, heads: int, topk: int, swa_topk: int = 0) -> tuple[int, int]:
+    """(num_splits, workspace_bytes) for a decode of ``tokens`` query tokens
+    (``swa_topk`` window rows per token add one partial slot)."""
     splits = ctypes.c_int32(0)
     nbytes = ctypes.c_size_t(0)
-    _lib.check(_lib.load().rm_sparse_decode_workspace(tokens, heads, topk, ctypes.byref(splits),
-                                                       ctypes.byref(nbytes)),
-               "rm_sparse_decode_workspace")
+    _lib.check(_lib.load().rm_sparse_decode_workspace_swa(tokens, heads, topk, swa_topk,
+                                                           ctypes.byref(splits),
+                                                           ctypes.byref(nbytes)),
+               "rm_sparse_decode_workspace_swa")
     return splits.value, nbytes.value
 
 
+def _swa_args(swa_pool, swa_indices, swa_lengths, batch, q_len):
+    """Validate the window inputs: (pool pages, indices, lengths, W)."""
+    if swa_pool is None and swa_indices is None:
+        return None, None, None, 0
+    if swa_pool is None or swa_indices is None:
+        raise ValueError("swa_pool and swa_indices are given together")
+    sbuf, spacked, _ = _as_pool(swa_pool, None)
+    if spacked:
+        raise ValueError("the window rows are read from a Native pool")
+    if swa_indices.dtype != torch.int32 or swa_indices.dim() != 3 \
+            or swa_indices.shape[:2] != (batch, q_len) or not swa_indices.is_contiguous():
+        raise ValueError("swa_indices must be a contiguous int32 [batch, q_len, W] tensor")
+    width = swa_indices.shape[-1]
+    if width > 512:
+        raise ValueError("at most 512 window rows per token")
+    if swa_lengths is not None and (swa_lengths.dtype != torch.int32
+                                    or swa_lengths.numel() != batch * q_len
+                                    or not swa_lengths.is_contiguous()):
+        raise ValueError(f"swa_lengths must be a contiguous int32 tensor of {batch * q_len} entries")
+    return sbuf, swa_indices, swa_lengths, width
+
+
 def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length, sink,
-            freqs_cis, softmax_scale, out, lse, workspace, layer_id):
+            freqs_cis, softmax_scale, out, lse, workspace, layer_id, swa_pool=None,
+            swa_indices=None, swa_lengths=None):
     buf, is_packed, keep = _as_pool(pool, layer_id)
     if is_packed != packed:
         raise ValueError("pool format does not match the decode reader")
@@ -76,18 +108,32 @@ def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length
         raise ValueError("out must be a contiguous bfloat16 tensor shaped like q")
     if lse.shape != (batch, q_len, heads) or lse.dtype != torch.float32 or not lse.is_contiguous():
         raise ValueError("lse must be a contiguous float32 [batch, q_len, heads] tensor")
+    sbuf, sidx, slen, width = _swa_args(swa_pool, swa_indices, swa_lengths, batch, q_len)
     # a single request's table may be a broadcast view (stride 0 in dim 0)
     bt_stride = block_table.stride(0) if batch > 1 else max(block_table.stride(0),
                                                             block_table.shape[1])
-    _, need = get_decode_metadata(batch * q_len, heads, topk)
+    _, need = get_decode_metadata(batch * q_len, heads, topk, width)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
-    _check_cuda(q, buf, block_table, indices, seqlens, topk_length, sink, freqs_cis, out, lse)
+    _check_cuda(q, buf, block_table, indices, seqlens, topk_length, sink, freqs_cis, out, lse,
+                sbuf, sidx, slen)
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     ws_ptr = ptr(workspace) if need else None
     ws_bytes = workspace.numel() * workspace.element_size() if need else 0
     lib = _lib.load()
-    if packed:
+    if width > 0:
+        common = (q.data_ptr(), batch, q_len, heads, buf.data_ptr(), buf.shape[0],
+                  block_table.data_ptr(), bt_stride, block_table.shape[1], ptr(seqlens),
+                  indices.data_ptr(), topk, ptr(topk_length), sbuf.data_ptr(), sbuf.shape[0],
+                  sidx.data_ptr(), width, ptr(slen), ptr(sink))
+        tail = (float(softmax_scale), out.data_ptr(), lse.data_ptr(), ws_ptr, ws_bytes, _stream())
+        if packed:
+            _lib.check(lib.rm_remnant_sparse_decode_swa_fwd(*common, freq_ptr, freq_rows, *tail),
+                       "rm_remnant_sparse_decode_swa_fwd")
+        else:
+            _lib.check(lib.rm_native_sparse_decode_swa_fwd(*common, *tail),
+                       "rm_native_sparse_decode_swa_fwd")
+    elif packed:
         status = lib.rm_remnant_sparse_decode_fwd(
             q.data_ptr(), batch, q_len, heads, buf.data_ptr(), buf.shape[0],
             block_table.data_ptr(), bt_stride, block_table.shape[1], ptr(seqlens),
@@ -106,22 +152,26 @@ def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length
 
 def remnant_sparse_decode_fwd(q, pool, block_table, indices, *, seqlens=None, topk_length=None,
                               sink=None, freqs_cis=None, softmax_scale=None, out=None, lse=None,
-                              workspace=None, layer_id=None):
-    """Direct packed sparse-MLA decode. Returns (out [B, Sq, H, 512] bf16, lse [B, Sq, H])."""
+                              workspace=None, layer_id=None, swa_pool=None, swa_indices=None,
+                              swa_lengths=None):
+    """Direct packed sparse-MLA decode (with the window rows when ``swa_pool``
+    is given). Returns (out [B, Sq, H, 512] bf16, lse [B, Sq, H])."""
     return _decode(True, q, pool, block_table, indices, seqlens=seqlens,
                    topk_length=topk_length, sink=sink, freqs_cis=freqs_cis,
                    softmax_scale=softmax_scale, out=out, lse=lse, workspace=workspace,
-                   layer_id=layer_id)
+                   layer_id=layer_id, swa_pool=swa_pool, swa_indices=swa_indices,
+                   swa_lengths=swa_lengths)
 
 
 def native_sparse_decode_fwd(q, pool, block_table, indices, *, seqlens=None, topk_length=None,
                              sink=None, softmax_scale=None, out=None, lse=None, workspace=None,
-                             layer_id=None):
+                             layer_id=None, swa_pool=None, swa_indices=None, swa_lengths=None):
     """Native 584-byte control decode on the same harness."""
     return _decode(False, q, pool, block_table, indices, seqlens=seqlens,
                    topk_length=topk_length, sink=sink, freqs_cis=None,
                    softmax_scale=softmax_scale, out=out, lse=lse, workspace=workspace,
-                   layer_id=layer_id)
+                   layer_id=layer_id, swa_pool=swa_pool, swa_indices=swa_indices,
+                   swa_lengths=swa_lengths)
 
 
 def sparse_decode_fwd(q, pool, block_table, indices, **kwargs):

@@ -33,6 +33,12 @@
  *                             stock FlashMLA sparse FP8 decode on 584-B records
  *                             (Native control, same harness)
  *   rm_sparse_decode_workspace  FlashMLA get_mla_metadata-style split planning
+ *   rm_remnant_sparse_decode_swa_fwd / rm_native_sparse_decode_swa_fwd /
+ *   rm_sparse_decode_workspace_swa
+ *                             the same decodes attending the sliding-window (SWA)
+ *                             rows jointly with the C4 top-k and the sink, as the
+ *                             reference decode does (decode-store timing.json
+ *                             swa_length 64; joint softmax training/losses.py:393-398)
  *   rm_pack_rows_k / rm_unpack_gather_bf16_k
  *                             the survivor-profile store and reader
  *                             (configure_cache_format(..., keep_count=K) with the
@@ -168,6 +174,46 @@ int rm_native_sparse_decode_fwd(const uint16_t* q, int64_t batch, int64_t q_len,
                                 const int32_t* topk_length, const float* sink,
                                 float softmax_scale, uint16_t* out, float* lse,
                                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Split planning for the decodes below: as rm_sparse_decode_workspace, plus one
+ * partial slot per row for the window rows when swa_topk > 0 (swa_topk <= 512).
+ * num_splits counts every slot. */
+int rm_sparse_decode_workspace_swa(int64_t tokens, int64_t heads, int64_t topk,
+                                   int64_t swa_topk, int32_t* num_splits,
+                                   size_t* workspace_bytes);
+
+/* Direct decode with the sliding window: token t attends, in one softmax with
+ * the sink, its C4 top-k (as rm_remnant_sparse_decode_fwd) and the window rows
+ * swa_indices[t, 0 .. swa_length[t]) (NULL lengths = swa_topk): slots of
+ * swa_pool, a Native pool (584-byte records in 64-record pages, tail stored
+ * rotated). A slot < 0 or >= swa_pool_pages * 64 contributes nothing.
+ * swa_topk <= 512; with window rows topk <= 32256 (63 splits of 512 records,
+ * the window taking the 64th partial slot); swa_topk == 0 is
+ * rm_remnant_sparse_decode_fwd. */
+int rm_remnant_sparse_decode_swa_fwd(const uint16_t* q, int64_t batch, int64_t q_len,
+                                     int64_t heads, const uint8_t* pool, int64_t pool_pages,
+                                     const int32_t* block_table, int64_t block_table_stride,
+                                     int64_t max_blocks, const int32_t* seqlens,
+                                     const int32_t* indices, int64_t topk,
+                                     const int32_t* topk_length, const uint8_t* swa_pool,
+                                     int64_t swa_pool_pages, const int32_t* swa_indices,
+                                     int64_t swa_topk, const int32_t* swa_length,
+                                     const float* sink, const float* freqs, int64_t freq_rows,
+                                     float softmax_scale, uint16_t* out, float* lse,
+                                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Native control decode with the sliding window (same contract, 584-byte C4 records). */
+int rm_native_sparse_decode_swa_fwd(const uint16_t* q, int64_t batch, int64_t q_len,
+                                    int64_t heads, const uint8_t* pool, int64_t pool_pages,
+                                    const int32_t* block_table, int64_t block_table_stride,
+                                    int64_t max_blocks, const int32_t* seqlens,
+                                    const int32_t* indices, int64_t topk,
+                                    const int32_t* topk_length, const uint8_t* swa_pool,
+                                    int64_t swa_pool_pages, const int32_t* swa_indices,
+                                    int64_t swa_topk, const int32_t* swa_length,
+                                    const float* sink, float softmax_scale, uint16_t* out,
+                                    float* lse, void* workspace, size_t workspace_bytes,
+                                    void* stream);
 
 #ifdef __cplusplus
 }

@@ -92,6 +92,10 @@ def lib():
         _lib.orc_sink_attention.argtypes = [vp, i64, vp, vp, i64, vp, f32, vp, vp]
         _lib.orc_sparse_decode.argtypes = [vp, i64, i64, i64, vp, i64, ctypes.c_int, vp, i64,
                                            i64, vp, vp, i64, vp, vp, vp, i64, f32, vp, vp]
+        _lib.orc_swa_gather.argtypes = [vp, i64, vp, i64, i64, vp, vp]
+        _lib.orc_sparse_decode_swa.argtypes = [vp, i64, i64, i64, vp, i64, ctypes.c_int, vp,
+                                               i64, i64, vp, vp, i64, vp, vp, i64, vp, i64, vp,
+                                               vp, vp, i64, f32, vp, vp]
     return _lib
 
 
@@ -305,6 +309,45 @@ def sparse_decode(q_bits, pool, packed: bool, block_table, seqlens, indices, top
         _p(q), batch, q_len, heads, _p(pool), pool.size // page_bytes, int(packed), _p(bt),
         bt.shape[1], bt.shape[1], _p(None if seqlens is None else _c(seqlens, np.int32)),
         _p(idx), topk, _p(None if topk_length is None else _c(topk_length, np.int32)),
+        _p(None if sink is None else _c(sink, np.float32)), _p(f),
+        0 if f is None else f.size // (ROPE_PAIRS * 2), scale, _p(out), _p(lse))
+    return out, lse
+
+
+def swa_gather(swa_pool, slots, length=None):
+    """SWA rows of one token from a Native pool: (bf16 bits [K, 512], valid [K])."""
+    pool = _c(swa_pool, np.uint8)
+    sl = _c(slots, np.int32)
+    rows = np.zeros((sl.size, HEAD_DIM), np.uint16)
+    valid = np.zeros(sl.size, np.uint8)
+    lib().orc_swa_gather(_p(pool), pool.size // NATIVE_PAGE_BYTES, _p(sl), sl.size,
+                         sl.size if length is None else int(length), _p(rows), _p(valid))
+    return rows, valid.astype(bool)
+
+
+def sparse_decode_swa(q_bits, pool, packed: bool, block_table, seqlens, indices, topk_length,
+                      swa_pool, swa_indices, swa_length, sink, freqs, scale: float):
+    """Decode step attending the SWA rows (Native pool slots swa_indices
+    [B, Sq, W], swa_length [B*Sq] or None) jointly with the C4 top-k."""
+    q = _c(q_bits, np.uint16)
+    batch, q_len, heads, _ = q.shape
+    idx = _c(indices, np.int32)
+    topk = idx.shape[-1]
+    sidx = _c(swa_indices, np.int32)
+    swa_topk = sidx.shape[-1]
+    bt = _c(block_table, np.int32)
+    pool = _c(pool, np.uint8)
+    spool = _c(swa_pool, np.uint8)
+    page_bytes = PAGE_BYTES if packed else NATIVE_PAGE_BYTES
+    out = np.zeros((batch, q_len, heads, HEAD_DIM), np.float64)
+    lse = np.zeros((batch, q_len, heads), np.float64)
+    f = None if freqs is None else _c(freqs, np.float32)
+    lib().orc_sparse_decode_swa(
+        _p(q), batch, q_len, heads, _p(pool), pool.size // page_bytes, int(packed), _p(bt),
+        bt.shape[1], bt.shape[1], _p(None if seqlens is None else _c(seqlens, np.int32)),
+        _p(idx), topk, _p(None if topk_length is None else _c(topk_length, np.int32)),
+        _p(spool), spool.size // NATIVE_PAGE_BYTES, _p(sidx), swa_topk,
+        _p(None if swa_length is None else _c(swa_length, np.int32)),
         _p(None if sink is None else _c(sink, np.float32)), _p(f),
         0 if f is None else f.size // (ROPE_PAIRS * 2), scale, _p(out), _p(lse))
     return out, lse

@@ -449,3 +449,54 @@ void orc_sparse_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t 
     free(rows);
     free(valid);
 }
+
+/* SWA rows of one token: the rows lie in a Native pool (64-record pages) at
+ * physical slots swa_slots[k]; valid[k] = 0 for k >= length or a slot outside
+ * the pool. Rows are stored with the tail already rotated. */
+void orc_swa_gather(const uint8_t* swa_pool, int64_t swa_pages, const int32_t* swa_slots,
+                    int64_t nk, int64_t length, uint16_t* rows, uint8_t* valid) {
+    for (int64_t k = 0; k < nk; ++k) {
+        uint16_t* o = rows + k * HEAD_DIM;
+        int64_t sl = swa_slots[k];
+        int ok = k < length && sl >= 0 && sl < swa_pages * PAGE_RECORDS;
+        valid[k] = (uint8_t)ok;
+        if (!ok) { memset(o, 0, HEAD_DIM * 2); continue; }
+        const uint8_t* pg = swa_pool + page_of(sl) * NATIVE_PAGE_BYTES;
+        int in = (int)(sl % PAGE_RECORDS);
+        orc_native_unpack_row(pg + in * NATIVE_DATA_BYTES,
+                              pg + PAGE_RECORDS * NATIVE_DATA_BYTES + in * SCALE_BYTES, o);
+    }
+}
+
+/* Decode step with the sliding-window rows attended jointly (training/losses.py:
+ * 393-398: softmax over cat(swa rows, C4 rows) plus the sink): token t attends
+ * its swa_topk SWA slots (swa_length[t] of them valid; NULL = all) and its
+ * C4 top-k exactly as orc_sparse_decode does, in one softmax. */
+void orc_sparse_decode_swa(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads,
+                           const uint8_t* pool, int64_t pool_pages, int packed,
+                           const int32_t* block_table, int64_t bt_stride, int64_t max_blocks,
+                           const int32_t* seqlens, const int32_t* indices, int64_t topk,
+                           const int32_t* topk_length, const uint8_t* swa_pool,
+                           int64_t swa_pages, const int32_t* swa_indices, int64_t swa_topk,
+                           const int32_t* swa_length, const float* sink, const float* freqs,
+                           int64_t freq_rows, float scale, double* out, double* lse) {
+    int64_t nk = swa_topk + topk;
+    uint16_t* rows = (uint16_t*)malloc(sizeof(uint16_t) * HEAD_DIM * (nk > 0 ? nk : 1));
+    uint8_t* valid = (uint8_t*)malloc(nk > 0 ? nk : 1);
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t s = 0; s < q_len; ++s) {
+            int64_t t = b * q_len + s;
+            int64_t len = topk_length ? topk_length[t] : topk;
+            int64_t swa_len = swa_length ? swa_length[t] : swa_topk;
+            orc_swa_gather(swa_pool, swa_pages, swa_indices + t * swa_topk, swa_topk, swa_len,
+                           rows, valid);
+            orc_decode_gather(pool, pool_pages, packed, block_table + b * bt_stride, 1,
+                              max_blocks, seqlens ? seqlens[b] : INT64_MAX,
+                              indices + t * topk, topk, len, freqs, freq_rows,
+                              rows + swa_topk * HEAD_DIM, valid + swa_topk);
+            orc_sink_attention(q + t * heads * HEAD_DIM, heads, rows, valid, nk, sink, scale,
+                               out + t * heads * HEAD_DIM, lse + t * heads);
+        }
+    free(rows);
+    free(valid);
+}

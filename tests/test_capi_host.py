@@ -96,6 +96,23 @@ def test_capi_rejects_bad_arguments_without_launching():
                                           ctypes.byref(nbytes)) == -2
     assert lib.rm_sparse_decode_workspace(1, 16, 32768, ctypes.byref(splits),
                                           ctypes.byref(nbytes)) == 0 and splits.value == 64
+    # window rows take one partial slot: the C4 list keeps 63 splits of 512
+    assert lib.rm_sparse_decode_workspace_swa(1, 16, 32256, 64, ctypes.byref(splits),
+                                              ctypes.byref(nbytes)) == 0 and splits.value == 64
+    assert lib.rm_sparse_decode_workspace_swa(1, 16, 32257, 64, ctypes.byref(splits),
+                                              ctypes.byref(nbytes)) == -2
+    assert lib.rm_sparse_decode_workspace_swa(1, 16, 512, 513, ctypes.byref(splits),
+                                              ctypes.byref(nbytes)) == -2
+    assert lib.rm_sparse_decode_workspace_swa(300, 16, 512, 64, ctypes.byref(splits),
+                                              ctypes.byref(nbytes)) == 0
+    assert splits.value == 2 and nbytes.value == 300 * 2 * 16 * 513 * 4
+    swa_args = [x, 1, 1, 16, pool, 1, s, 4, 4, None, s, 8, None, None, 0, s, 8, None, None,
+                None, 0, 0.1, x, w, None, 0, None]
+    assert lib.rm_remnant_sparse_decode_swa_fwd(*swa_args) == -1  # window slots without a pool
+    swa_args[13], swa_args[14] = pool + 8, 1
+    assert lib.rm_remnant_sparse_decode_swa_fwd(*swa_args) == -3  # unaligned window pool
+    swa_args[13], swa_args[16] = pool, 600
+    assert lib.rm_remnant_sparse_decode_swa_fwd(*swa_args) == -2  # window above 512
 
 
 def test_decode_split_plan():
@@ -215,6 +232,32 @@ def test_pool_planes_and_capacity():
     packed, native = remnant.records_fitting(hbm, "direct"), remnant.records_fitting(hbm, "native")
     assert abs(packed / 878.0e6 - 1) < 1e-3 and abs(native / 493.2e6 - 1) < 1e-3
     assert abs(packed / native - 584 / 328) < 1e-3
+
+
+def test_decode_window_rows_host_validation():
+    pool = remnant.LatentPool(1, device="cpu")
+    native = remnant.LatentPool(1, fmt="native", device="cpu")
+    q = torch.zeros((2, 1, 16, 512), dtype=torch.bfloat16)
+    bt = torch.zeros((2, 1), dtype=torch.int32)
+    idx = torch.zeros((2, 1, 4), dtype=torch.int32)
+    sidx = torch.zeros((2, 1, 64), dtype=torch.int32)
+    with pytest.raises(ValueError, match="together"):
+        remnant.remnant_sparse_decode_fwd(q, pool, bt, idx, swa_pool=native)
+    with pytest.raises(ValueError, match="Native pool"):
+        remnant.remnant_sparse_decode_fwd(q, pool, bt, idx, swa_pool=pool, swa_indices=sidx)
+    with pytest.raises(ValueError, match="swa_indices"):
+        remnant.remnant_sparse_decode_fwd(q, pool, bt, idx, swa_pool=native,
+                                          swa_indices=sidx[:1])
+    with pytest.raises(ValueError, match="512"):
+        remnant.remnant_sparse_decode_fwd(q, pool, bt, idx, swa_pool=native,
+                                          swa_indices=torch.zeros((2, 1, 513), dtype=torch.int32))
+    with pytest.raises(ValueError, match="swa_lengths"):
+        remnant.remnant_sparse_decode_fwd(q, pool, bt, idx, swa_pool=native, swa_indices=sidx,
+                                          swa_lengths=torch.zeros(3, dtype=torch.int32))
+    with pytest.raises(ValueError, match="GPU"):
+        remnant.remnant_sparse_decode_fwd(q, pool, bt, idx, swa_pool=native, swa_indices=sidx)
+    assert remnant.get_decode_metadata(300, 16, 512, 64) == (2, 300 * 2 * 16 * 513 * 4)
+    assert remnant.get_decode_metadata(300, 16, 512) == (1, 0)
 
 
 def test_survivor_profile_pools():

@@ -303,11 +303,37 @@ def build_decode_case(contexts, q_len, heads, topk, seed, packed=True, sink=True
                 contexts=contexts, packed=packed)
 
 
+def add_swa(c, width, seed, lengths=None, swa_pages=4):
+    """Window rows for every token: a Native pool of swa_pages pages written by
+    the Native store (tail rotated at its slot's position), per-token slots
+    with padding (-1) and out-of-pool entries, optional valid counts."""
+    tokens = c["q"].shape[0] * c["q"].shape[1]
+    rows = swa_pages * 64
+    x = syn.latents(rows, seed=seed)
+    spool = remnant.LatentPool(swa_pages, fmt="native", device=DEV)
+    freqs = syn.rope_freqs(4 * rows).to(DEV)
+    slots = torch.arange(rows, dtype=torch.int32, device=DEV)
+    remnant.native_store_rows(x.to(DEV), torch.ones(512, device=DEV), 1e-6, slots, slots, freqs,
+                              spool)
+    rng = np.random.default_rng(seed)
+    sidx = rng.integers(0, rows, (tokens, width)).astype(np.int32)
+    sidx[:, ::9] = -1
+    sidx[:, 4::13] = rows + 7  # outside the pool
+    c["swa_pool"] = spool
+    c["swa_idx"] = sidx.reshape(c["q"].shape[0], c["q"].shape[1], width)
+    c["swa_lens"] = None if lengths is None else np.asarray(lengths, np.int32).reshape(tokens)
+    return c
+
+
 def run_decode(c):
     q = c["q"].to(DEV)
     kw = dict(seqlens=torch.tensor(c["contexts"], dtype=torch.int32, device=DEV),
               topk_length=torch.from_numpy(c["lens"]).to(DEV),
               sink=None if c["sink"] is None else c["sink"].to(DEV))
+    if c.get("swa_pool") is not None:
+        kw.update(swa_pool=c["swa_pool"], swa_indices=torch.from_numpy(c["swa_idx"]).to(DEV),
+                  swa_lengths=None if c["swa_lens"] is None
+                  else torch.from_numpy(c["swa_lens"]).to(DEV))
     bt = torch.from_numpy(c["table"]).to(DEV)
     idx = torch.from_numpy(c["idx"]).to(DEV)
     if c["packed"]:
@@ -321,6 +347,13 @@ def run_decode(c):
 
 def oracle_decode(c):
     pool = c["pool"].layer().cpu().numpy()
+    if c.get("swa_pool") is not None:
+        return oracle.sparse_decode_swa(
+            syn.bf16_bits(c["q"]).reshape(c["q"].shape), pool, c["packed"], c["table"],
+            np.array(c["contexts"], np.int32), c["idx"], c["lens"],
+            c["swa_pool"].layer().cpu().numpy(), c["swa_idx"], c["swa_lens"],
+            None if c["sink"] is None else c["sink"].numpy(),
+            torch.view_as_real(c["freqs"]).numpy() if c["packed"] else None, 1 / np.sqrt(512))
     return oracle.sparse_decode(
         syn.bf16_bits(c["q"]).reshape(c["q"].shape), pool, c["packed"], c["table"],
         np.array(c["contexts"], np.int32), c["idx"], c["lens"],
@@ -416,4 +449,49 @@ def test_decode_maximum_topk():
     """Top-k 32768, the entry point's limit: 64 splits of 512 records."""
     banner("decode topk=32768")
     c = build_decode_case([33000], q_len=1, heads=16, topk=32768, seed=23, sink=False)
+    check_decode(c)
+
+
+# ---- sliding-window rows attended jointly ---------------------------------------------------
+
+@pytest.mark.parametrize("packed", [True, False], ids=["direct", "native"])
+def test_decode_swa_joint_with_padding_lengths_and_sink(packed):
+    """Window of 64 rows per token (padding, out-of-pool slots, lengths 64,
+    10 and 0) attended with the C4 top-k and the sink in one softmax."""
+    banner(f"decode swa joint packed={packed}")
+    c = build_decode_case([300, 70, 1000], q_len=1, heads=16, topk=256, seed=31, packed=packed)
+    add_swa(c, 64, seed=32, lengths=[64, 10, 0])
+    check_decode(c)
+
+
+def test_decode_swa_reference_shape_h64_b16():
+    """The reference's decode case: 64 heads, batch 16, top-k 512 with 317 valid,
+    64 window rows (decode-store timing.json h64_b16_k317)."""
+    banner("decode swa H=64 B=16 topk=512/317")
+    ctx = syn.log_uniform_contexts(16, 2048, 16384, 33)
+    c = build_decode_case(ctx, q_len=1, heads=64, topk=512, seed=33)
+    c["lens"][:] = 317
+    add_swa(c, 64, seed=34)
+    check_decode(c)
+
+
+def test_decode_swa_only_and_window_128_next_n2():
+    """Empty C4 selections (only the window and the sink remain) and a
+    128-row window with two query tokens per request."""
+    banner("decode swa only / window 128")
+    c = build_decode_case([500, 900], q_len=2, heads=16, topk=128, seed=35)
+    c["lens"][:] = 0
+    add_swa(c, 128, seed=36)
+    check_decode(c)
+
+
+def test_decode_swa_large_batch_row_combine():
+    """256 tokens: the C4 plan has one split per token, so the window split
+    brings in the workspace and the per-row combine."""
+    banner("decode swa B=256")
+    ctx = syn.log_uniform_contexts(256, 2048, 8192, 37)
+    c = build_decode_case(ctx, q_len=1, heads=16, topk=512, seed=37)
+    add_swa(c, 64, seed=38)
+    assert remnant.get_decode_metadata(256, 16, 512)[0] == 1
+    assert remnant.get_decode_metadata(256, 16, 512, 64)[0] == 2
     check_decode(c)

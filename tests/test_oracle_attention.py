@@ -110,3 +110,60 @@ def test_decode_gather_through_block_table_matches_unpack_gather():
                                          1 / np.sqrt(512))
     np.testing.assert_array_equal(out[0, 0], ref)
     np.testing.assert_array_equal(lse[0, 0], ref_lse)
+
+
+def test_joint_swa_decode_matches_reference_formula():
+    """training/losses.py:393-398: rows = cat(swa, C4 rows); probabilities =
+    softmax(cat(q rows^T * scale, sink))[..., :-1]; out = probabilities @ rows,
+    evaluated with torch in float64. SWA rows come from a Native pool by
+    physical slot; slots past swa_length or outside the pool are skipped."""
+    rng = np.random.default_rng(11)
+    pages, swa_pages = 4, 2
+    x = oracle.synthetic_latents(pages * 64, seed=12)
+    pool = np.zeros((pages, oracle.PAGE_BYTES), np.uint8)
+    oracle.pack_rows_paged(x, np.ones(512, np.float32), 1e-6,
+                           np.arange(pages * 64, dtype=np.int32), pool)
+    sx = oracle.synthetic_latents(swa_pages * 64, seed=13)
+    spool = np.zeros((swa_pages, oracle.NATIVE_PAGE_BYTES), np.uint8)
+    freqs = oracle.rope_table(4 * 256)
+    oracle.native_pack_rows_paged(sx, np.ones(512, np.float32), 1e-6,
+                                  np.arange(swa_pages * 64, dtype=np.int32),
+                                  np.arange(swa_pages * 64, dtype=np.int32), freqs, spool)
+    block_table = np.arange(pages, dtype=np.int32)[None]
+    idx = rng.choice(256, 48, replace=False).astype(np.int32)
+    swa = rng.choice(128, 20, replace=False).astype(np.int32)
+    swa[3] = 128 * 5  # outside the SWA pool
+    swa[7] = -1
+    q = bf16(rng.standard_normal((1, 1, 16, 512)) * 0.3)
+    sink = rng.standard_normal(16).astype(np.float32)
+    scale = float(np.float32(1 / np.sqrt(512)))
+    out, lse = oracle.sparse_decode_swa(q, pool, True, block_table, None, idx[None, None], None,
+                                        spool, swa[None, None], np.array([18], np.int32), sink,
+                                        freqs, scale)
+    # independent assembly of the rows: Native records by slot, C4 rows by unpack_gather
+    swa_rows = []
+    for k, sl in enumerate(swa[:18]):
+        if 0 <= sl < 128:
+            pg, inn = divmod(int(sl), 64)
+            page = spool[pg]
+            swa_rows.append(oracle.native_unpack_row(page[inn * 576:(inn + 1) * 576],
+                                                     page[64 * 576 + inn * 8:64 * 576 + inn * 8 + 8]))
+    c4 = oracle.unpack_gather(pool, idx[None], idx[None], np.array([48]), freqs)
+    rows = torch.from_numpy(oracle.bf16_to_f32(np.concatenate([np.stack(swa_rows), c4]))
+                            .astype(np.float64))
+    qf = torch.from_numpy(oracle.bf16_to_f32(q[0, 0]).astype(np.float64))
+    logits = qf @ rows.T * scale
+    s = torch.from_numpy(sink.astype(np.float64))[:, None]
+    prob = torch.softmax(torch.cat([logits, s], 1), 1)[:, :-1]
+    np.testing.assert_allclose(out[0, 0], (prob @ rows).numpy(), rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(lse[0, 0], torch.logsumexp(torch.cat([logits, s], 1), 1).numpy(),
+                               rtol=1e-12)
+    assert len(swa_rows) == 16
+    # no SWA rows: identical to the plain decode
+    none, none_lse = oracle.sparse_decode_swa(q, pool, True, block_table, None, idx[None, None],
+                                              None, spool, swa[None, None], np.array([0], np.int32),
+                                              sink, freqs, scale)
+    plain, plain_lse = oracle.sparse_decode(q, pool, True, block_table, None, idx[None, None],
+                                            None, sink, freqs, scale)
+    np.testing.assert_array_equal(none, plain)
+    np.testing.assert_array_equal(none_lse, plain_lse)
