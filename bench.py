@@ -62,6 +62,8 @@ def parse():
     p.add_argument("--quick", action="store_true", help="skip decode, capacity and CPU legs")
     p.add_argument("--no-capacity", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--prefill-only", action="store_true",
+                   help="only the prefill-read reconstruction and the Adapter")
     p.add_argument("--no-reference-shapes", action="store_true",
                    help="skip the reference's H64/H128 decode shapes")
     p.add_argument("--cpu-sample", type=int, default=196608)
@@ -301,6 +303,71 @@ def reference_shapes_leg(torch, remnant):
     return res
 
 
+def prefill_leg(torch, remnant):
+    """The reference's prefill-read reconstruction (history 143,360 tokens =
+    35,840 C4 records, shuffled physical order, raw positions for the RoPE
+    rows; dsv4-flash-prefill-read README.md) and the Adapter at the decode
+    shape H64/B16/top-k 512, each timed from HIP-graph replays of 20 calls."""
+    dev = "cuda"
+    n = 35840
+    g = torch.Generator(device=dev).manual_seed(20260919)
+    x = (torch.randn(n, 512, device=dev, generator=g) * 2).to(torch.bfloat16)
+    slots = torch.randperm(n, device=dev, generator=g).to(torch.int32)
+    pool = remnant.LatentPool((n + 63) // 64, device=dev)
+    remnant.pack_rows_fused(x, torch.ones(512, device=dev), 1e-6, slots, pool)
+    raw = torch.arange(n, dtype=torch.int32, device=dev).view(1, n)
+    physical = slots.view(1, n)
+    lengths = torch.full((1,), n, dtype=torch.int32, device=dev)
+    freqs = remnant.synthetic.rope_freqs(4 * n).to(dev)
+    out = torch.empty((n, 512), dtype=torch.bfloat16, device=dev)
+
+    def timed(fn, calls=20, samples=10):
+        # HIP-graph replays of `calls` calls: host launch cost stays out of the
+        # figure (an eager Python call costs more than these kernels run)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(calls):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(samples):
+            e = events(torch, 2)
+            e[0].record()
+            graph.replay()
+            e[1].record()
+            e[1].synchronize()
+            times.append(e[0].elapsed_time(e[1]) * 1e3 / calls)
+        return statistics.median(times)
+
+    rope_us = timed(lambda: remnant.unpack_gather_bf16(pool, physical, raw, lengths, freqs, out,
+                                                       fused_rope=True))
+    plain_us = timed(lambda: remnant.unpack_gather_bf16(pool, physical, None, lengths, None, out))
+    byt = n * (328 + 4 + 1024)
+    res = {"prefill_read_35840": {
+        "records": n, "reconstruct_rope_us": rope_us, "reconstruct_us": plain_us,
+        "GBps": byt / (plain_us * 1e3), "GBps_rope_with_table": (byt + n * 260) / (rope_us * 1e3),
+        "reference_h100_us": {"fused_unpack_rope": 89.50, "split_unpack": 77.34,
+                              "split_rope": 25.28, "native_dequant": 69.31}}}
+    # Adapter: 16 tokens x 512 selections of the same pool into a Native workspace
+    rows = 16 * 512
+    sel = torch.randint(0, n, (16, 512), device=dev, generator=g, dtype=torch.int32)
+    sel_raw = sel.clone()
+    sel_len = torch.full((16,), 512, dtype=torch.int32, device=dev)
+    native = remnant.LatentPool(rows // 64, fmt="native", device=dev)
+    ad_us = timed(lambda: remnant.packed_to_native(pool, sel, sel_raw, sel_len, freqs, native))
+    res["adapter_h64_b16_k512"] = {"rows": rows, "us": ad_us,
+                                   "GBps": rows * (328 + 256 + 8 + 584) / (ad_us * 1e3)}
+    return res
+
+
 def cpu_leg(args):
     """Oracle (plain C, one thread) on a bounded sample of the bulk workload."""
     import numpy as np
@@ -344,6 +411,9 @@ def main():
     torch.cuda.set_device(0)
     if args.decode_only:
         print(json.dumps({"decode": decode_leg(torch, remnant, args)}), flush=True)
+        return
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_leg(torch, remnant)}), flush=True)
         return
     log(f"bulk pack + reconstruct, {args.records} records")
     b = bulk(torch, remnant, args)
@@ -402,6 +472,8 @@ def main():
     }
     if not args.quick:
         line["decode"] = decode_leg(torch, remnant, args)
+        log("prefill read + adapter")
+        line["prefill"] = prefill_leg(torch, remnant)
     if not (args.quick or args.no_cpu):
         log("cpu baseline (oracle, one thread)")
         line["cpu_baseline"] = cpu_leg(args)

@@ -161,6 +161,58 @@ def unpack_gather_bf16(packed_buffers, physical_indices: torch.Tensor,
     return output
 
 
+def packed_to_native(packed_buffers, physical_indices: torch.Tensor,
+                     raw_indices: torch.Tensor | None, topk_lengths: torch.Tensor,
+                     freqs_cis: torch.Tensor | None, native_output, *,
+                     layer_id: int | None = None):
+    """Adapter (the reference's CUDA Adapter, third_party/README.md:259): the
+    rows ``unpack_gather_bf16`` would return, each written as a Native 584-byte
+    record at workspace row q * k_sel + k of ``native_output`` (a Native
+    ``LatentPool`` or uint8 [pages, 37376] tensor with >= ceil(rows / 64)
+    pages), for a stock Native decode to read. Invalid selections become the
+    Native encoding of a zero row. 256-survivor pools only, as in the reference."""
+    buf, packed, keep = _as_pool(packed_buffers, layer_id)
+    if not packed:
+        raise ValueError("packed_to_native reads the Packed (remnant) format")
+    if keep != config.KEEP_COUNT:
+        raise ValueError("the Adapter reads 256-survivor records only")
+    nbuf, npacked, _ = _as_pool(native_output, None)
+    if npacked:
+        raise ValueError("native_output must be a Native pool")
+    if raw_indices is not None and physical_indices.shape != raw_indices.shape:
+        raise ValueError("physical_indices and raw_indices must have equal shape")
+    if physical_indices.dim() != 2:
+        raise ValueError("indices must be [queries, k]")
+    for name, t in (("physical_indices", physical_indices), ("raw_indices", raw_indices),
+                    ("topk_lengths", topk_lengths)):
+        if t is not None and t.dtype != torch.int32:
+            raise ValueError(f"{name} must be int32")
+    n_queries, selected_k = physical_indices.shape
+    if topk_lengths.dim() != 1 or topk_lengths.shape[0] != n_queries:
+        raise ValueError("topk_lengths must be [queries]")
+    if n_queries * selected_k > nbuf.shape[0] * config.PAGE_RECORDS:
+        raise ValueError("native_output has fewer records than queries * k")
+    freq_ptr, freq_rows = None, 0
+    if freqs_cis is not None:
+        if freqs_cis.dtype != torch.complex64 or not freqs_cis.is_contiguous():
+            raise ValueError("freqs_cis must be a contiguous complex64 tensor")
+        if raw_indices is None:
+            raise ValueError("raw_indices are required with freqs_cis")
+        freq_ptr = freqs_cis.data_ptr()
+        freq_rows = freqs_cis.numel() // (config.ROPE_DIM // 2)
+    if n_queries * selected_k == 0:
+        return native_output
+    _check_cuda(buf, physical_indices, raw_indices, topk_lengths, nbuf, freqs_cis)
+    _lib.check(_lib.load().rm_packed_to_native(
+        buf.data_ptr(), buf.shape[0], physical_indices.data_ptr(), physical_indices.stride(0),
+        physical_indices.stride(1), None if raw_indices is None else raw_indices.data_ptr(),
+        0 if raw_indices is None else raw_indices.stride(0),
+        0 if raw_indices is None else raw_indices.stride(1), topk_lengths.data_ptr(),
+        topk_lengths.stride(0), n_queries, selected_k, freq_ptr, freq_rows, nbuf.data_ptr(),
+        nbuf.shape[0], _stream()), "rm_packed_to_native")
+    return native_output
+
+
 def unpack_rows(pool, slots: torch.Tensor, *, layer_id: int | None = None) -> torch.Tensor:
     """Pre-RoPE BF16 rows [n, 512] of pool slots (exact dequantization)."""
     slots = slots.to(torch.int32).reshape(1, -1).contiguous()

@@ -39,6 +39,9 @@
  *                             rows jointly with the C4 top-k and the sink, as the
  *                             reference decode does (decode-store timing.json
  *                             swa_length 64; joint softmax training/losses.py:393-398)
+ *   rm_packed_to_native       the CUDA Adapter (SGLang csrc/remnant/packed_to_native.cu,
+ *                             third_party/README.md:259, 289) and the Triton
+ *                             _bf16_to_native_kernel step of the Triton decode
  *   rm_pack_rows_k / rm_unpack_gather_bf16_k
  *                             the survivor-profile store and reader
  *                             (configure_cache_format(..., keep_count=K) with the
@@ -134,6 +137,20 @@ int rm_unpack_gather_bf16_k(const uint8_t* pool, int64_t pool_pages, int keep_co
                             const int32_t* lengths, int64_t length_stride, int64_t n_queries,
                             int64_t selected_k, const float* freqs, int64_t freq_rows,
                             uint16_t* out, void* stream);
+
+/* Adapter: the rows rm_unpack_gather_bf16 would produce (same gather,
+ * validity and RoPE rules; invalid rows are zero rows), each re-encoded as a
+ * Native 584-byte record (seven UE8M0/E4M3 NoPE groups from the row's own
+ * BF16 values, the tail as BF16, scale row = 7 bytes + a zero pad) at
+ * workspace row q * selected_k + k of `native`, a Native page layout of
+ * native_pages pages (>= ceil(n_queries * selected_k / 64)). Re-encoding a
+ * dequantized Packed row is exact. 256-survivor pools only. */
+int rm_packed_to_native(const uint8_t* pool, int64_t pool_pages, const int32_t* physical,
+                        int64_t physical_stride_q, int64_t physical_stride_k,
+                        const int32_t* raw, int64_t raw_stride_q, int64_t raw_stride_k,
+                        const int32_t* lengths, int64_t length_stride, int64_t n_queries,
+                        int64_t selected_k, const float* freqs, int64_t freq_rows,
+                        uint8_t* native, int64_t native_pages, void* stream);
 
 /* Split planning for the sparse decode of `tokens` query tokens with `topk`
  * selected records each and `heads` query heads. Writes the number of split-KV

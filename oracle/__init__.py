@@ -92,6 +92,9 @@ def lib():
         _lib.orc_sink_attention.argtypes = [vp, i64, vp, vp, i64, vp, f32, vp, vp]
         _lib.orc_sparse_decode.argtypes = [vp, i64, i64, i64, vp, i64, ctypes.c_int, vp, i64,
                                            i64, vp, vp, i64, vp, vp, vp, i64, f32, vp, vp]
+        _lib.orc_native_encode_row.argtypes = [vp, vp, vp]
+        _lib.orc_packed_to_native.argtypes = [vp, i64, vp, i64, i64, vp, i64, i64, vp, i64, i64,
+                                              i64, vp, i64, vp]
         _lib.orc_swa_gather.argtypes = [vp, i64, vp, i64, i64, vp, vp]
         _lib.orc_sparse_decode_swa.argtypes = [vp, i64, i64, i64, vp, i64, ctypes.c_int, vp,
                                                i64, i64, vp, vp, i64, vp, vp, i64, vp, i64, vp,
@@ -312,6 +315,30 @@ def sparse_decode(q_bits, pool, packed: bool, block_table, seqlens, indices, top
         _p(None if sink is None else _c(sink, np.float32)), _p(f),
         0 if f is None else f.size // (ROPE_PAIRS * 2), scale, _p(out), _p(lse))
     return out, lse
+
+
+def native_encode_row(row_bits):
+    """Native record (data [576], scales [8]) of a BF16 row."""
+    data = np.zeros(NATIVE_DATA_BYTES, np.uint8)
+    scales = np.zeros(SCALE_BYTES, np.uint8)
+    lib().orc_native_encode_row(_p(_c(row_bits, np.uint16)), _p(data), _p(scales))
+    return data, scales
+
+
+def packed_to_native(pool, physical, raw, lengths, freqs=None) -> np.ndarray:
+    """Adapter: Native pages [ceil(Q*K/64), 37376] holding row (q, k) of the
+    gather at workspace row q * K + k."""
+    pool = _c(pool, np.uint8)
+    phys = _c(np.asarray(physical, np.int32), np.int32)
+    raw_c = None if raw is None else _c(np.asarray(raw, np.int32), np.int32)
+    lens = _c(lengths, np.int32)
+    nq, nk = phys.shape
+    out = np.zeros(((nq * nk + 63) // 64, NATIVE_PAGE_BYTES), np.uint8)
+    f = None if freqs is None else _c(freqs, np.float32)
+    lib().orc_packed_to_native(_p(pool), pool.size // PAGE_BYTES, _p(phys), nk, 1, _p(raw_c), nk,
+                               1, _p(lens), 1, nq, nk, _p(f),
+                               0 if f is None else f.size // (ROPE_PAIRS * 2), _p(out))
+    return out
 
 
 def swa_gather(swa_pool, slots, length=None):

@@ -331,6 +331,22 @@ void orc_native_pack_row(const float* x, const float* w, float eps, const float*
     scales[NOPE_DIM / GROUP] = 0;
 }
 
+/* Native record of a dense BF16 row (the dense BF16 -> Native conversion
+ * `_bf16_to_native_kernel` of the reference's Triton decode, launch list in
+ * benchmarks/microbench/dsv4-flash-decode-store/profiling/h64_b16_k512/
+ * metrics.json; the CUDA Adapter, third_party/README.md:259): nope groups 0..6 as
+ * UE8M0/E4M3 from the row's own BF16 values, the tail copied as stored, scale
+ * row = 7 bytes + one zero pad byte. A zero row gives zero codes and scale
+ * bytes 105 (the 1e-4 amax floor). */
+void orc_native_encode_row(const uint16_t* row, uint8_t* data, uint8_t* scales) {
+    uint8_t codes[HEAD_DIM], sb[NGROUPS];
+    quantize_groups(row, 0, NOPE_DIM / GROUP, codes, sb);
+    memcpy(data, codes, NOPE_DIM);
+    memcpy(data + NOPE_DIM, row + NOPE_DIM, (HEAD_DIM - NOPE_DIM) * 2);
+    memcpy(scales, sb, NOPE_DIM / GROUP);
+    scales[NOPE_DIM / GROUP] = 0;
+}
+
 void orc_native_pack_rows_paged(const float* x, const float* w, float eps,
                                 const int32_t* slot, const int32_t* position,
                                 const float* freqs, int64_t freq_rows, int64_t rows,
@@ -499,4 +515,24 @@ void orc_sparse_decode_swa(const uint16_t* q, int64_t batch, int64_t q_len, int6
         }
     free(rows);
     free(valid);
+}
+
+/* Adapter (Packed -> Native workspace, third_party/README.md:259, 289): row
+ * (q, k) of unpack_gather_bf16 (same gather, validity and RoPE rules; invalid
+ * rows are zero rows) re-encoded as a Native record at workspace row
+ * q * nk + k (page row / 64, slot row % 64 of a Native page layout). */
+void orc_packed_to_native(const uint8_t* pool, int64_t pool_pages, const int32_t* physical,
+                          int64_t ps_q, int64_t ps_k, const int32_t* raw, int64_t rs_q,
+                          int64_t rs_k, const int32_t* lengths, int64_t ls, int64_t nq,
+                          int64_t nk, const float* freqs, int64_t freq_rows, uint8_t* out) {
+    uint16_t* rows = (uint16_t*)malloc(sizeof(uint16_t) * HEAD_DIM * (nq * nk > 0 ? nq * nk : 1));
+    orc_unpack_gather(pool, pool_pages, physical, ps_q, ps_k, raw, rs_q, rs_k, lengths, ls, nq,
+                      nk, freqs, freq_rows, rows);
+    for (int64_t i = 0; i < nq * nk; ++i) {
+        uint8_t* pg = out + page_of(i) * NATIVE_PAGE_BYTES;
+        int in = (int)(i % PAGE_RECORDS);
+        orc_native_encode_row(rows + i * HEAD_DIM, pg + in * NATIVE_DATA_BYTES,
+                              pg + PAGE_RECORDS * NATIVE_DATA_BYTES + in * SCALE_BYTES);
+    }
+    free(rows);
 }

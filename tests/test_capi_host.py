@@ -234,6 +234,33 @@ def test_pool_planes_and_capacity():
     assert abs(packed / native - 584 / 328) < 1e-3
 
 
+def test_adapter_host_validation():
+    lib = _lib.load()
+    _, pool = buf(21000)
+    _, s = buf(64)
+    _, out = buf(37376)
+    assert lib.rm_packed_to_native(pool, 1, s, 1, 1, None, 0, 0, s, 1, 0, 5, None, 0, out, 1,
+                                   None) == 0  # empty: no launch
+    assert lib.rm_packed_to_native(pool, 1, s, 65, 1, None, 0, 0, s, 1, 2, 65, None, 0, out, 2,
+                                   None) == -2  # 130 rows do not fit two pages
+    assert lib.rm_packed_to_native(pool, 1, s, 1, 1, None, 0, 0, s, 1, 2, 5, None, 0, out + 8, 1,
+                                   None) == -3
+    packed = remnant.LatentPool(1, device="cpu")
+    native = remnant.LatentPool(1, fmt="native", device="cpu")
+    idx = torch.zeros((2, 40), dtype=torch.int32)
+    lengths = torch.full((2,), 40, dtype=torch.int32)
+    with pytest.raises(ValueError, match="Native pool"):
+        remnant.packed_to_native(packed, idx, idx, lengths, None, packed)
+    with pytest.raises(ValueError, match="fewer records"):
+        remnant.packed_to_native(packed, torch.zeros((2, 40), dtype=torch.int32), None, lengths,
+                                 None, native)
+    with pytest.raises(ValueError, match="256-survivor"):
+        remnant.packed_to_native(remnant.LatentPool(1, device="cpu", keep_count=192), idx[:1],
+                                 None, lengths[:1], None, native)
+    with pytest.raises(ValueError, match="GPU"):
+        remnant.packed_to_native(packed, idx[:1], None, lengths[:1], None, native)
+
+
 def test_decode_window_rows_host_validation():
     pool = remnant.LatentPool(1, device="cpu")
     native = remnant.LatentPool(1, fmt="native", device="cpu")

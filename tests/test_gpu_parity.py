@@ -132,6 +132,32 @@ def test_unpack_gather_bit_exact_with_rope_invalid_and_strided():
     assert np.array_equal(syn.bf16_bits(out2), expect2)
 
 
+@pytest.mark.parametrize("keep_count", [256, 448])
+def test_unpack_gather_bulk_call_70000_rows(keep_count):
+    """A call of at least 16,384 rows takes the four-rows-per-wave path (smaller
+    calls use one row per wave): bit-exact with RoPE, invalid entries included."""
+    banner(f"unpack_gather 70000 rows keep {keep_count}")
+    pages = 64
+    x = syn.latents(pages * 64, seed=44)
+    slots = np.random.default_rng(44).permutation(pages * 64).astype(np.int32)
+    pool = gpu_pack(x, slots, pages, keep_count=keep_count)
+    ref_pool = pool.layer().cpu().numpy()
+    rng = np.random.default_rng(45)
+    nq, nk = 7, 10000
+    physical = rng.integers(-5, pages * 64 + 5, (nq, nk)).astype(np.int32)
+    raw = rng.integers(-1, 1100, (nq, nk)).astype(np.int32)
+    lengths = np.array([10000, 9000, 1, 0, 10000, 5000, 9999], np.int32)
+    freqs = syn.rope_freqs(4 * 1024)
+    out = torch.empty((nq * nk, 512), dtype=torch.bfloat16, device=DEV)
+    remnant.unpack_gather_bf16(pool, torch.from_numpy(physical).to(DEV),
+                               torch.from_numpy(raw).to(DEV), torch.from_numpy(lengths).to(DEV),
+                               freqs.to(DEV), out)
+    torch.cuda.synchronize()
+    expect = oracle.unpack_gather(ref_pool, physical, raw, lengths,
+                                  torch.view_as_real(freqs).numpy(), keep_count=keep_count)
+    assert np.array_equal(syn.bf16_bits(out), expect)
+
+
 def test_reconstruct_roundtrip_all_records():
     """pack -> unpack_rows equals the oracle's dense simulation of every record."""
     banner("reconstruct round trip")
@@ -160,6 +186,74 @@ def test_native_store_bit_exact():
     oracle.native_pack_rows_paged(x.float().numpy(), W1, 1e-6, slots, positions,
                                   torch.view_as_real(freqs).numpy(), ref)
     assert np.array_equal(pool.layer().cpu().numpy(), ref)
+
+
+# ---- Adapter: Packed -> Native workspace --------------------------------------------------
+
+def test_adapter_bit_exact_with_rope_invalid_and_strided():
+    """rm_packed_to_native against the oracle, byte for byte: strided indices,
+    invalid selections (Native encoding of a zero row), a partial last page."""
+    banner("adapter packed -> native")
+    pages = 6
+    x = syn.latents(pages * 64, seed=41)
+    slots = np.random.default_rng(41).permutation(pages * 64).astype(np.int32)
+    pool = gpu_pack(x, slots, pages)
+    ref_pool = pool.layer().cpu().numpy()
+    rng = np.random.default_rng(42)
+    nq, nk = 3, 150
+    physical = rng.integers(-2, pages * 64 + 3, (nq, nk)).astype(np.int32)
+    raw = rng.integers(-1, 100, (nq, nk)).astype(np.int32)
+    lengths = np.array([150, 61, 0], np.int32)
+    freqs = syn.rope_freqs(4 * 96)
+    wide = torch.zeros((nq, 2 * nk), dtype=torch.int32)
+    wide[:, ::2] = torch.from_numpy(physical)
+    out_pages = (nq * nk + 63) // 64 + 1  # one spare page stays untouched
+    native = remnant.LatentPool(out_pages, fmt="native", device=DEV)
+    native.buffer.fill_(0x3C)
+    remnant.packed_to_native(pool, wide.to(DEV)[:, ::2], torch.from_numpy(raw).to(DEV),
+                             torch.from_numpy(lengths).to(DEV), freqs.to(DEV), native)
+    torch.cuda.synchronize()
+    expect = oracle.packed_to_native(ref_pool, physical, raw, lengths,
+                                     torch.view_as_real(freqs).numpy())
+    got = native.layer().cpu().numpy()
+    rows = nq * nk
+    for i in range(rows):  # every written record, data row and scale row
+        pg, r = divmod(i, 64)
+        assert np.array_equal(got[pg, r * 576:(r + 1) * 576], expect[pg, r * 576:(r + 1) * 576]), i
+        so = 64 * 576 + r * 8
+        assert np.array_equal(got[pg, so:so + 8], expect[pg, so:so + 8]), i
+    assert np.all(got[-1] == 0x3C)
+
+
+def test_adapter_then_native_decode_matches_direct_decode():
+    """The Adapter's workspace read by the Native decode (logical record k of
+    token t = workspace row t * K + k) gives the Direct decode's attention."""
+    banner("adapter + native decode")
+    c = build_decode_case([900, 300, 2000, 700], q_len=1, heads=16, topk=256, seed=43)
+    tokens, k_sel = 4, 256
+    bt = torch.from_numpy(c["table"]).to(DEV)
+    idx = torch.from_numpy(c["idx"]).to(DEV).view(tokens, k_sel)
+    lens = torch.from_numpy(c["lens"]).to(DEV).view(tokens)
+    ctx = torch.tensor(c["contexts"], dtype=torch.int32, device=DEV)
+    ok = (idx >= 0) & (idx < ctx[:, None]) & \
+        (torch.arange(k_sel, device=DEV)[None] < lens[:, None])
+    safe = torch.where(ok, idx, torch.zeros_like(idx))  # in-table for the gather below
+    physical = torch.where(ok, bt.gather(1, (safe // 64).long()) * 64 + safe % 64,
+                           torch.full_like(idx, -1)).to(torch.int32)
+    native = remnant.LatentPool(tokens * k_sel // 64, fmt="native", device=DEV)
+    remnant.packed_to_native(c["pool"], physical, idx.contiguous(), lens, c["freqs"].to(DEV),
+                             native)
+    table = torch.arange(tokens * 4, dtype=torch.int32, device=DEV).view(tokens, 4)
+    local = torch.where(ok, torch.arange(k_sel, device=DEV, dtype=torch.int32)[None].expand(tokens, -1),
+                        torch.full_like(idx, -1)).contiguous().view(tokens, 1, k_sel)
+    out, lse = remnant.native_sparse_decode_fwd(c["q"].to(DEV), native, table, local,
+                                                sink=c["sink"].to(DEV))
+    torch.cuda.synchronize()
+    ref, ref_lse = oracle_decode(c)
+    got = out.float().cpu().numpy()
+    assert np.abs(got - ref).max() <= OUT_TOL
+    assert syn.cosine(got, ref) >= COS_MIN
+    assert np.abs(lse.cpu().numpy() - ref_lse).max() <= OUT_TOL
 
 
 # ---- survivor profiles 64..448 (count + 72 byte records) ------------------------------------

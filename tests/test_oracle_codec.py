@@ -403,3 +403,37 @@ def test_survivor_count_outside_profiles_is_rejected():
     for bad in (0, 32, 200, 512):
         with pytest.raises(ValueError):
             oracle.select_keep(np.zeros((1, 512), np.float32), bad)
+
+
+# ---- Adapter: Packed -> Native workspace ------------------------------------------
+
+def test_adapter_is_lossless_and_encodes_invalid_rows_as_zero_rows():
+    """Re-encoding a dequantized Packed row as a Native record loses nothing:
+    each group's values are E4M3 codes times 2^e, so the Native scale is 2^e or
+    2^(e-1) and every code re-encodes exactly. Decoding the Adapter's records
+    gives back unpack_gather_bf16's rows bit for bit (tail included); invalid
+    selections are the Native encoding of a zero row (codes 0, scale bytes 105)."""
+    src = oracle.synthetic_latents(128, seed=14)
+    src[5] = 0.0
+    src[6, :8] = 1e-3  # tiny group maxima: the 1e-4 floor and subnormal codes
+    src[6, 8:] = 0.0
+    pool = np.zeros((2, oracle.PAGE_BYTES), np.uint8)
+    oracle.pack_rows_paged(src, np.linspace(0.5, 1.5, 512).astype(np.float32), 1e-6,
+                           np.arange(128, dtype=np.int32), pool)
+    rng = np.random.default_rng(15)
+    physical = rng.integers(-3, 131, (3, 50)).astype(np.int32)
+    physical[0, :3] = [5, 6, 7]
+    raw = rng.integers(0, 40, (3, 50)).astype(np.int32)
+    lengths = np.array([50, 20, 0], np.int32)
+    freqs = oracle.rope_table(4 * 32)  # raw >= 32 is beyond the table
+    rows = oracle.unpack_gather(pool, physical, raw, lengths, freqs)
+    native = oracle.packed_to_native(pool, physical, raw, lengths, freqs)
+    assert native.shape == (3, oracle.NATIVE_PAGE_BYTES)
+    for i in range(150):
+        page, slot = divmod(i, 64)
+        data = native[page, slot * 576:(slot + 1) * 576]
+        scales = native[page, 64 * 576 + slot * 8:64 * 576 + slot * 8 + 8]
+        assert np.array_equal(oracle.native_unpack_row(data, scales), rows[i]), i
+        if not rows[i].any():
+            assert not data.any() and list(scales) == [105] * 7 + [0]
+    assert sum(not r.any() for r in rows) > 20
