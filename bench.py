@@ -368,6 +368,38 @@ def prefill_leg(torch, remnant):
     return res
 
 
+def host_cache_leg(torch, remnant):
+    """Host-cache transfers: 262,144 scattered records of one layer backed up
+    to pinned host memory and restored, Packed (328 B) and Native (584 B)."""
+    dev = "cuda"
+    n = 262144
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(7)
+    for fmt in ("remnant", "native"):
+        pool = remnant.LatentPool(n // 64, fmt=fmt, device=dev)
+        host = remnant.HostLatentPool.like(pool)
+        d = torch.randperm(n, device=dev, generator=g).to(torch.int32)
+        h = torch.randperm(n, device=dev, generator=g).to(torch.int32)
+        out = {}
+        for name, fn in (("backup", lambda: host.backup_from_device_all_layer(pool, h, d)),
+                         ("restore", lambda: host.load_to_device_all_layer(pool, h, d))):
+            for _ in range(2):
+                fn()
+            torch.cuda.synchronize()
+            e = events(torch, 2)
+            e[0].record()
+            for _ in range(5):
+                fn()
+            e[1].record()
+            e[1].synchronize()
+            ms = e[0].elapsed_time(e[1]) / 5
+            out[name] = {"ms": ms, "GBps": n * pool.record_bytes / (ms * 1e6)}
+        res["packed" if fmt == "remnant" else "native"] = out
+        del pool, host
+    res["records"] = n
+    return res
+
+
 def cpu_leg(args):
     """Oracle (plain C, one thread) on a bounded sample of the bulk workload."""
     import numpy as np
@@ -413,7 +445,8 @@ def main():
         print(json.dumps({"decode": decode_leg(torch, remnant, args)}), flush=True)
         return
     if args.prefill_only:
-        print(json.dumps({"prefill": prefill_leg(torch, remnant)}), flush=True)
+        print(json.dumps({"prefill": prefill_leg(torch, remnant),
+                          "host_cache": host_cache_leg(torch, remnant)}), flush=True)
         return
     log(f"bulk pack + reconstruct, {args.records} records")
     b = bulk(torch, remnant, args)
@@ -474,6 +507,8 @@ def main():
         line["decode"] = decode_leg(torch, remnant, args)
         log("prefill read + adapter")
         line["prefill"] = prefill_leg(torch, remnant)
+        log("host cache transfers")
+        line["host_cache"] = host_cache_leg(torch, remnant)
     if not (args.quick or args.no_cpu):
         log("cpu baseline (oracle, one thread)")
         line["cpu_baseline"] = cpu_leg(args)

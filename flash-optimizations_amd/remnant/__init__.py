@@ -12,6 +12,7 @@ from .flash_mla import (get_decode_metadata, native_sparse_decode_fwd,
                         remnant_sparse_decode_fwd, sparse_decode_fwd)
 from .packed import (native_store_rows, pack_rows_fused, packed_to_native, unpack_gather_bf16,
                      unpack_rows)
+from .host_cache import HostLatentPool, copy_records
 from .pool import LatentPool, records_fitting
 
 __all__ = [
@@ -19,5 +20,5 @@ __all__ = [
     "native_sparse_decode_fwd", "remnant_sparse_decode_fwd", "sparse_decode_fwd",
     "native_store_rows", "pack_rows_fused", "packed_to_native", "unpack_gather_bf16",
     "unpack_rows",
-    "LatentPool", "records_fitting",
+    "LatentPool", "records_fitting", "HostLatentPool", "copy_records",
 ]

@@ -38,6 +38,8 @@ SIGNATURES = {
                                        _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
     "rm_packed_to_native": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
                                    _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "rm_copy_records": (_i32, [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i32,
+                               _i32, _vp]),
     "rm_sparse_decode_workspace": (_i32, [_i64, _i64, _i64, ctypes.POINTER(ctypes.c_int32),
                                           ctypes.POINTER(ctypes.c_size_t)]),
     "rm_remnant_sparse_decode_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64,

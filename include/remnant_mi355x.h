@@ -42,6 +42,9 @@
  *   rm_packed_to_native       the CUDA Adapter (SGLang csrc/remnant/packed_to_native.cu,
  *                             third_party/README.md:259, 289) and the Triton
  *                             _bf16_to_native_kernel step of the Triton decode
+ *   rm_copy_records           the host-cache (HiCache) coordinated value/bitmap/scale
+ *                             transfers (srt/mem_cache/memory_pool_host.py,
+ *                             third_party/README.md:261)
  *   rm_pack_rows_k / rm_unpack_gather_bf16_k
  *                             the survivor-profile store and reader
  *                             (configure_cache_format(..., keep_count=K) with the
@@ -74,6 +77,8 @@ enum rm_status {
 };
 
 enum rm_dtype { RM_F32 = 0, RM_BF16 = 1 };
+
+enum rm_format { RM_FORMAT_PACKED = 0, RM_FORMAT_NATIVE = 1 };
 
 #define RM_HEAD_DIM 512
 #define RM_NOPE_DIM 448
@@ -151,6 +156,19 @@ int rm_packed_to_native(const uint8_t* pool, int64_t pool_pages, const int32_t* 
                         const int32_t* lengths, int64_t length_stride, int64_t n_queries,
                         int64_t selected_k, const float* freqs, int64_t freq_rows,
                         uint8_t* native, int64_t native_pages, void* stream);
+
+/* Record transfer between two pools of one format (host-cache backup and
+ * restore): for i < n and every layer l < layers, record src_slots[i] of layer
+ * l of `src` is copied to record dst_slots[i] of layer l of `dst` -- the whole
+ * Packed record (codes, bitmap and scales together; format RM_FORMAT_PACKED
+ * with its keep_count) or the Native data row and scale row
+ * (RM_FORMAT_NATIVE). Pairs with a slot < 0 or beyond its pool are skipped.
+ * Layer l of a pool starts l * layer_bytes after its base. Either pool may be
+ * device memory or pinned host memory (hipHostMalloc). 8-byte alignment. */
+int rm_copy_records(const uint8_t* src, int64_t src_pages, int64_t src_layer_bytes,
+                    const int32_t* src_slots, uint8_t* dst, int64_t dst_pages,
+                    int64_t dst_layer_bytes, const int32_t* dst_slots, int64_t n,
+                    int64_t layers, int format, int keep_count, void* stream);
 
 /* Split planning for the sparse decode of `tokens` query tokens with `topk`
  * selected records each and `heads` query heads. Writes the number of split-KV

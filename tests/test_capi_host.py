@@ -234,6 +234,34 @@ def test_pool_planes_and_capacity():
     assert abs(packed / native - 584 / 328) < 1e-3
 
 
+def test_record_transfer_host_validation():
+    lib = _lib.load()
+    _, a = buf(21000)
+    _, b = buf(21000)
+    _, s = buf(64)
+    assert lib.rm_copy_records(a, 1, 0, s, b, 1, 0, s, 0, 1, 0, 256, None) == 0  # empty
+    assert lib.rm_copy_records(a, 1, 0, s, b, 1, 0, s, 4, 1, 2, 256, None) == -4  # format
+    assert lib.rm_copy_records(a, 1, 0, s, b, 1, 0, s, 4, 1, 0, 512, None) == -2  # no profile
+    assert lib.rm_copy_records(a + 4, 1, 0, s, b, 1, 0, s, 4, 1, 0, 256, None) == -3
+    assert lib.rm_copy_records(a, 1, 100, s, b, 1, 20992, s, 4, 2, 0, 256, None) == -2
+    assert lib.rm_copy_records(None, 1, 0, s, b, 1, 0, s, 4, 1, 1, 256, None) == -1
+    dev = remnant.LatentPool(2, layers=3, device="cpu")
+    host = remnant.HostLatentPool.like(dev, pin_memory=False)
+    assert host.buffer.shape == (3, 2, 20992) and host.rows == 128
+    h448 = remnant.HostLatentPool(1, fmt="remnant", keep_count=448, pin_memory=False)
+    assert h448.page_bytes == 64 * 520
+    idx = torch.zeros(4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="different record formats"):
+        remnant.copy_records(dev, idx, h448, idx)
+    with pytest.raises(ValueError, match="layer count"):
+        remnant.copy_records(dev, idx, remnant.HostLatentPool(2, 1, pin_memory=False), idx)
+    with pytest.raises(ValueError, match="equal length"):
+        remnant.copy_records(dev, idx, host, idx[:2])
+    with pytest.raises(ValueError, match="GPU"):
+        host.backup_from_device_all_layer(dev, idx, idx)
+    remnant.copy_records(dev, idx[:0], host, idx[:0])  # empty: nothing happens
+
+
 def test_adapter_host_validation():
     lib = _lib.load()
     _, pool = buf(21000)

@@ -256,6 +256,71 @@ def test_adapter_then_native_decode_matches_direct_decode():
     assert np.abs(lse.cpu().numpy() - ref_lse).max() <= OUT_TOL
 
 
+# ---- host cache: record backup and restore ---------------------------------------------------
+
+@pytest.mark.parametrize("fmt,keep_count", [("remnant", 256), ("remnant", 448), ("native", 256)])
+def test_host_cache_backup_and_restore_round_trip(fmt, keep_count):
+    """Backup of scattered records of every layer into a pinned host pool, then
+    restore into other slots of a fresh device pool: the moved records are
+    byte-identical (codes, bitmap and scales together; Native data and scale
+    rows), nothing else is written, skipped pairs leave canaries intact."""
+    banner(f"host cache {fmt} keep {keep_count}")
+    layers, pages = 3, 4
+    rows = pages * 64
+    dev = remnant.LatentPool(pages, layers=layers, fmt=fmt, device=DEV, keep_count=keep_count)
+    g = torch.Generator(device=DEV).manual_seed(51)
+    dev.buffer.copy_(torch.randint(0, 256, dev.buffer.shape, generator=g, device=DEV,
+                                   dtype=torch.int32).to(torch.uint8))
+    host = remnant.HostLatentPool(6, layers=layers, fmt=fmt, keep_count=keep_count)
+    host.buffer.fill_(0xA5)
+    rng = np.random.default_rng(52)
+    n = 150
+    dslots = rng.choice(rows, n, replace=False).astype(np.int32)
+    hslots = rng.choice(6 * 64, n, replace=False).astype(np.int32)
+    dslots[7], hslots[9] = -1, 6 * 64 + 3  # skipped pairs
+    d_t, h_t = torch.from_numpy(dslots).to(DEV), torch.from_numpy(hslots).to(DEV)
+    host.backup_from_device_all_layer(dev, h_t, d_t)
+    torch.cuda.synchronize()
+    back = remnant.LatentPool(pages, layers=layers, fmt=fmt, device=DEV, keep_count=keep_count)
+    back.buffer.fill_(0x5A)
+    host.load_to_device_all_layer(back, h_t, d_t)
+    torch.cuda.synchronize()
+    ok = np.array([i not in (7, 9) for i in range(n)])
+    for layer in range(layers):
+        want = dev.records(torch.from_numpy(dslots[ok]).to(DEV), layer).cpu().numpy()
+        got_host = host_records(host, hslots[ok], layer)
+        assert np.array_equal(got_host, want)
+        got = back.records(torch.from_numpy(dslots[ok]).to(DEV), layer).cpu().numpy()
+        assert np.array_equal(got, want)
+    untouched = np.setdiff1d(np.arange(rows), dslots[ok])
+    rest = back.records(torch.from_numpy(untouched.astype(np.int32)).to(DEV), 1).cpu().numpy()
+    assert np.all(rest == 0x5A)
+    spare = np.setdiff1d(np.arange(6 * 64), hslots[ok])
+    assert np.all(host_records(host, spare, 0) == 0xA5)
+    # one layer only
+    one = remnant.LatentPool(pages, layers=layers, fmt=fmt, device=DEV, keep_count=keep_count)
+    host.load_to_device_per_layer(one, h_t, d_t, 2)
+    torch.cuda.synchronize()
+    assert np.array_equal(one.records(torch.from_numpy(dslots[ok]).to(DEV), 2).cpu().numpy(),
+                          dev.records(torch.from_numpy(dslots[ok]).to(DEV), 2).cpu().numpy())
+    assert int(one.buffer[0].count_nonzero()) == 0 and int(one.buffer[1].count_nonzero()) == 0
+
+
+def host_records(host, slots, layer):
+    """Records of a host pool (same layout as LatentPool.records)."""
+    pg = host.buffer[layer]
+    out = []
+    for s in slots:
+        page, row = divmod(int(s), 64)
+        if host.packed:
+            rb = host.page_bytes // 64
+            out.append(pg[page, row * rb:(row + 1) * rb].numpy())
+        else:
+            data = pg[page, row * 576:(row + 1) * 576].numpy()
+            out.append(np.concatenate([data, pg[page, 64 * 576 + row * 8:64 * 576 + row * 8 + 8].numpy()]))
+    return np.stack(out)
+
+
 # ---- survivor profiles 64..448 (count + 72 byte records) ------------------------------------
 
 KEEPS = [64, 128, 192, 256, 320, 384, 448]
