@@ -135,9 +135,15 @@ __device__ __forceinline__ void wait_vm_upto() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
 
-constexpr int kPcConsumers = 2;
 constexpr int kPcProducers = 4;
-constexpr int kPcThreads = 64 * (kPcConsumers + kPcProducers);
+constexpr int kPcMaxGroups = 2;            // 16-head groups per workgroup (1 or 2)
+// Consumer waves and threads of a workgroup serving kHG groups of 16 heads:
+// two consumer waves per group (one per half of the output coordinates).
+template <int kHG>
+struct PcRoles {
+  static constexpr int kConsumers = 2 * kHG;
+  static constexpr int kThreads = 64 * (kConsumers + kPcProducers);
+};
 constexpr int kPcStage = 32;               // records per stage: two 16-record tiles
 constexpr int kPcRing = 4;                 // K tile slots (two stages)
 constexpr int kPcKPitch = kHeadDim + 16;   // BF16 per K row (1056 B: rows 8 banks apart)
@@ -185,7 +191,7 @@ struct PcShared {
   uint64_t row_tab[kPcMaxChunk];
   uint64_t aux_tab[kPacked ? kPcMaxChunk : 1];
   uint64_t sel_tab[kPacked ? 256 : 1];
-  float mrg[kPcConsumers][2][16];  // consumers' (m_ref, l) per head
+  float mrg[2 * kPcMaxGroups][2][16];  // consumers' (reference, seen) maxima per head
 };
 constexpr size_t kPcSmemBytes = sizeof(PcShared<true>) > sizeof(PcShared<false>)
                                     ? sizeof(PcShared<true>) : sizeof(PcShared<false>);
@@ -201,11 +207,14 @@ __device__ __forceinline__ float max_over_rows(float x) {
 }
 
 // One workgroup's share: split `split` of list `a` (a C4 top-k list through
-// the block table, or with a.block_table == nullptr a list of pool slots).
-template <bool kPacked>
+// the block table, or with a.block_table == nullptr a list of pool slots), for
+// kHG groups of 16 heads: every expanded record serves all of them.
+template <bool kPacked, int kHG>
 __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>* sm,
                                           const int split) {
   using G = PcGeo<kPacked>;
+  constexpr int kPcConsumers = PcRoles<kHG>::kConsumers;
+  constexpr int kPcThreads = PcRoles<kHG>::kThreads;
   auto& ktile = sm->ktile;
   auto& raw = sm->raw;
   auto& sel_tab = sm->sel_tab;
@@ -217,7 +226,9 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
   const int lane = tid & 63;
   const int wv = uniform(tid >> 6);
   const int64_t t = blockIdx.y;
-  const int64_t head0 = (int64_t)blockIdx.z * 16;
+  const int64_t head_wg = (int64_t)blockIdx.z * 16 * kHG;
+  // a consumer's 16 heads (consumers 2 hg and 2 hg + 1 serve group hg)
+  const int64_t head0 = head_wg + (wv < kPcConsumers ? 16 * (wv >> 1) : 0);
   const int64_t b = t / a.q_len;
 
   int64_t len = a.topk;
@@ -225,8 +236,13 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     const int64_t l = a.topk_length[t];
     len = l < 0 ? 0 : (l < a.topk ? l : a.topk);
   }
-  const int64_t k0 = (int64_t)split * a.chunk;
-  const int64_t k1 = k0 + a.chunk < len ? k0 + a.chunk : len;
+  // this token's valid entries in whole stages, spread evenly over the splits
+  // (at most a.chunk each, since len <= topk): a short list finishes early in
+  // every split instead of emptying the last ones
+  const int64_t len_stages = (len + kPcStage - 1) / kPcStage;
+  const int64_t chunk = ((len_stages + a.splits - 1) / a.splits) * kPcStage;
+  const int64_t k0 = (int64_t)split * chunk;
+  const int64_t k1 = k0 + chunk < len ? k0 + chunk : len;
   const int n = k1 > k0 ? (int)(k1 - k0) : 0;
   const int stages = (n + kPcStage - 1) / kPcStage;
   const int64_t seqlen = a.seqlens ? a.seqlens[b] : INT64_MAX;
@@ -281,9 +297,12 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
   // workgroup-uniform decision every wave takes from LDS.
   auto redo_pass = [&](float& mtrue) {
     const int h = lane & 15;
-    const float r0 = mrg[0][0][h], r1 = mrg[1][0][h], t0 = mrg[0][1][h], t1 = mrg[1][1][h];
-    mtrue = fmaxf(t0, t1);
-    return __ballot(t0 > r0 + kRefSlack || t1 > r1 + kRefSlack) != 0;
+    bool over = false;
+#pragma unroll
+    for (int c = 0; c < kPcConsumers; ++c) over = over || mrg[c][1][h] > mrg[c][0][h] + kRefSlack;
+    const int c0 = wv < kPcConsumers ? wv & ~1 : 0;  // this consumer's group
+    mtrue = fmaxf(mrg[c0][1][h], mrg[c0 + 1][1][h]);
+    return __ballot(over) != 0;
   };
 
   // The two roles run separate loops with the same barrier sequence per pass
@@ -526,7 +545,7 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
   // Both consumers score every tile, so their softmax state (reference, sum)
   // is identical and each finalises its half of O on its own.
   const int g = lane >> 4, col = lane & 15;
-  const int half = wv;  // 0 or 1
+  const int half = wv & 1;  // 0 or 1
   f32x4 o[16];          // O[head 4g + i][256 half + 16 nt + col]
   float m_ref = -INFINITY, m_seen = -INFINITY, l_run = 0.0f;
 
@@ -672,31 +691,35 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
   }
 }
 
-__global__ __launch_bounds__(kPcThreads) void packed_decode_pc_kernel(DecodeArgs a) {
+template <int kHG>
+__global__ __launch_bounds__(PcRoles<kHG>::kThreads) void packed_decode_pc_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[sizeof(PcShared<true>)];
-  decode_pc<true>(a, reinterpret_cast<PcShared<true>*>(smem), blockIdx.x);
+  decode_pc<true, kHG>(a, reinterpret_cast<PcShared<true>*>(smem), blockIdx.x);
 }
-__global__ __launch_bounds__(kPcThreads) void native_decode_pc_kernel(DecodeArgs a) {
+template <int kHG>
+__global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_decode_pc_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[sizeof(PcShared<false>)];
-  decode_pc<false>(a, reinterpret_cast<PcShared<false>*>(smem), blockIdx.x);
+  decode_pc<false, kHG>(a, reinterpret_cast<PcShared<false>*>(smem), blockIdx.x);
 }
 // C4 list and window rows in one launch: workgroups x < c4.splits take a C4
 // split, the last column the window rows (Native records).
-template <bool kPacked>
+template <bool kPacked, int kHG>
 __device__ __forceinline__ void decode_joint(const DecodeArgs& c4, const DecodeArgs& swa) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kPcSmemBytes];
   if ((int)blockIdx.x < c4.splits)
-    decode_pc<kPacked>(c4, reinterpret_cast<PcShared<kPacked>*>(smem), blockIdx.x);
+    decode_pc<kPacked, kHG>(c4, reinterpret_cast<PcShared<kPacked>*>(smem), blockIdx.x);
   else
-    decode_pc<false>(swa, reinterpret_cast<PcShared<false>*>(smem), 0);
+    decode_pc<false, kHG>(swa, reinterpret_cast<PcShared<false>*>(smem), 0);
 }
-__global__ __launch_bounds__(kPcThreads) void packed_swa_decode_pc_kernel(DecodeArgs c4,
-                                                                         DecodeArgs swa) {
-  decode_joint<true>(c4, swa);
+template <int kHG>
+__global__ __launch_bounds__(PcRoles<kHG>::kThreads) void packed_swa_decode_pc_kernel(
+    DecodeArgs c4, DecodeArgs swa) {
+  decode_joint<true, kHG>(c4, swa);
 }
-__global__ __launch_bounds__(kPcThreads) void native_swa_decode_pc_kernel(DecodeArgs c4,
-                                                                         DecodeArgs swa) {
-  decode_joint<false>(c4, swa);
+template <int kHG>
+__global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_swa_decode_pc_kernel(
+    DecodeArgs c4, DecodeArgs swa) {
+  decode_joint<false, kHG>(c4, swa);
 }
 
 // Merge split partials with the sink, for many rows. One workgroup (4 waves)
@@ -830,9 +853,19 @@ struct Plan {
 // split, at most kPcMaxChunk records per split and max_splits splits (the
 // combine merges at most kMaxSplits partial slots per row, the window rows'
 // slot included).
+// 16-head groups per workgroup. Two groups share every expanded record (half
+// the expansion work per head) but double a workgroup's consumer work; that
+// pays once 16-head workgroups alone would fill the GPU's round of about 256
+// workgroups with at most two splits each (measured on the reference's decode
+// shapes: H128/B16 27.8 us with two groups vs 33.4 us with one; H128/B8 and
+// H64/B8-16 are 10-20 % faster with one).
+int head_groups(int64_t tokens, int64_t heads) {
+  return heads % (16 * kPcMaxGroups) == 0 && tokens * (heads / 16) >= 128 ? kPcMaxGroups : 1;
+}
+
 Plan plan_pc(int64_t tokens, int64_t heads, int64_t topk, int64_t max_splits = kMaxSplits,
              bool window = false) {
-  const int64_t base = tokens * (heads / 16);
+  const int64_t base = tokens * (heads / (16 * head_groups(tokens, heads)));
   const int64_t stages = (topk + kPcStage - 1) / kPcStage;
   int64_t splits = base > 0 ? (256 + base - 1) / base : 1;
   // the window rows' workgroups (one per token and head block) share the round
@@ -927,6 +960,9 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   a.ws_o = (float*)workspace;
   a.ws_lse = bytes ? (float*)workspace + (size_t)tokens * slots * heads * kHeadDim : nullptr;
   hipStream_t s = (hipStream_t)stream;
+  const int hg = head_groups(tokens, heads);
+  const dim3 block(hg == 2 ? PcRoles<2>::kThreads : PcRoles<1>::kThreads);
+  const unsigned zblocks = (unsigned)(heads / (16 * hg));
   if (w.topk > 0) {
     // the window rows are one more split, read by the Native path of the same launch
     DecodeArgs b = a;
@@ -942,13 +978,21 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
     b.chunk = kPcMaxChunk;
     b.splits = 1;
     b.ws_base = plan.splits;
-    hipLaunchKernelGGL(kPacked ? packed_swa_decode_pc_kernel : native_swa_decode_pc_kernel,
-                       dim3((unsigned)slots, (unsigned)tokens, (unsigned)(heads / 16)),
-                       dim3(kPcThreads), 0, s, a, b);
+    const dim3 grid((unsigned)slots, (unsigned)tokens, zblocks);
+    if (hg == 2)
+      hipLaunchKernelGGL(kPacked ? packed_swa_decode_pc_kernel<2> : native_swa_decode_pc_kernel<2>,
+                         grid, block, 0, s, a, b);
+    else
+      hipLaunchKernelGGL(kPacked ? packed_swa_decode_pc_kernel<1> : native_swa_decode_pc_kernel<1>,
+                         grid, block, 0, s, a, b);
   } else {
-    hipLaunchKernelGGL(kPacked ? packed_decode_pc_kernel : native_decode_pc_kernel,
-                       dim3((unsigned)plan.splits, (unsigned)tokens, (unsigned)(heads / 16)),
-                       dim3(kPcThreads), 0, s, a);
+    const dim3 grid((unsigned)plan.splits, (unsigned)tokens, zblocks);
+    if (hg == 2)
+      hipLaunchKernelGGL(kPacked ? packed_decode_pc_kernel<2> : native_decode_pc_kernel<2>, grid,
+                         block, 0, s, a);
+    else
+      hipLaunchKernelGGL(kPacked ? packed_decode_pc_kernel<1> : native_decode_pc_kernel<1>, grid,
+                         block, 0, s, a);
   }
   if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   if (slots > 1) {

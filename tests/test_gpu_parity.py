@@ -555,6 +555,20 @@ def test_decode_next_n2_and_32_heads():
     check_decode(c)
 
 
+@pytest.mark.parametrize("packed", [True, False], ids=["direct", "native"])
+def test_decode_head_groups_48_and_128_heads(packed):
+    """48 heads run as three 16-head workgroups; 128 heads over 16 tokens (at
+    least 128 token x 16-head blocks) as four 32-head workgroups per token, two
+    16-head groups sharing each expanded record."""
+    banner(f"decode H=48/128 packed={packed}")
+    for heads, contexts, q_len, seed in ((48, [1500, 600], 1, 18),
+                                         (128, [900, 1500, 600, 2000, 700, 1100, 1300, 800], 2, 19)):
+        c = build_decode_case(contexts, q_len=q_len, heads=heads, topk=512, seed=seed,
+                              packed=packed)
+        c["lens"][1] = 301
+        check_decode(c)
+
+
 def test_decode_empty_selection_gives_zero_and_sink_lse():
     banner("decode empty selection")
     c = build_decode_case([64], q_len=1, heads=16, topk=64, seed=14)
