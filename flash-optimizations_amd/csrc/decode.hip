@@ -722,22 +722,31 @@ __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_swa_decode_pc_k
   decode_joint<false, kHG>(c4, swa);
 }
 
-// Merge split partials with the sink, for many rows. One workgroup (4 waves)
-// per (token, head) row: wave w takes splits w, w+4, ...; lane l owns
-// coordinates 8l..8l+7; the 4 partial sums meet in LDS in a fixed order.
-__global__ __launch_bounds__(256) void combine_rows_kernel(const float* __restrict__ ws_o,
-                                                      const float* __restrict__ ws_lse,
-                                                      const float* __restrict__ sink, int splits,
-                                                      int64_t heads, uint16_t* __restrict__ out,
-                                                      float* __restrict__ lse) {
-  __shared__ f32x4 part[4][2][64];
+// Merge split partials with the sink, for many rows: one wave per (token,
+// head) row, lane l owning coordinates 8l..8l+7. The partial loads of up to
+// kWaveBatch splits are issued together with the split LSEs (lane s holds
+// split s), so a row costs one round trip per kWaveBatch splits.
+constexpr int kWaveBatch = 8;
+__global__ __launch_bounds__(256) void combine_wave_kernel(const float* __restrict__ ws_o,
+                                                           const float* __restrict__ ws_lse,
+                                                           const float* __restrict__ sink,
+                                                           int splits, int64_t heads, int64_t rows,
+                                                           uint16_t* __restrict__ out,
+                                                           float* __restrict__ lse) {
   const int lane = wave_lane();
-  const int wave = uniform((int)(threadIdx.x >> 6));
-  const int64_t row = blockIdx.x;
+  const int64_t row = (int64_t)blockIdx.x * 4 + uniform((int)(threadIdx.x >> 6));
+  if (row >= rows) return;
   const int64_t t = row / heads, h = row - t * heads;
-  const float sink2 = sink ? sink[h] * kLog2e : -INFINITY;
-  // every wave reads all split LSEs (lane s holds split s; splits <= 64)
+  const float* src = ws_o + (t * splits * heads + h) * kHeadDim + 8 * lane;
+  const int64_t step = heads * kHeadDim;
+  f32x4 x[2 * kWaveBatch];
+#pragma unroll
+  for (int u = 0; u < kWaveBatch; ++u) {
+    x[2 * u] = u < splits ? *(const f32x4*)(src + u * step) : f32x4{0.f, 0.f, 0.f, 0.f};
+    x[2 * u + 1] = u < splits ? *(const f32x4*)(src + u * step + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   const float ls = lane < splits ? ws_lse[(t * splits + lane) * heads + h] : -INFINITY;
+  const float sink2 = sink ? sink[h] * kLog2e : -INFINITY;
   float mz = fmaxf(ls, sink2);
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) mz = fmaxf(mz, __shfl_xor(mz, d, 64));
@@ -745,45 +754,39 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const float* __restri
   float z = w;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) z += __shfl_xor(z, d, 64);
-  const float* src = ws_o + (t * splits * heads + h) * kHeadDim + 8 * lane;
-  const int64_t step = heads * kHeadDim;
   f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
-  constexpr int kU = 4;  // splits per batch of in-flight loads, per wave
-  for (int s0 = wave; s0 < splits; s0 += 4 * kU) {
-    f32x4 x[2 * kU];
+  for (int s0 = 0; s0 < splits; s0 += kWaveBatch) {
+    if (s0 > 0) {
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int s = s0 + 4 * u;
-      x[2 * u] = s < splits ? *(const f32x4*)(src + s * step) : f32x4{0.f, 0.f, 0.f, 0.f};
-      x[2 * u + 1] = s < splits ? *(const f32x4*)(src + s * step + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u < kWaveBatch; ++u) {
+        const int sp = s0 + u;
+        x[2 * u] = sp < splits ? *(const f32x4*)(src + sp * step) : f32x4{0.f, 0.f, 0.f, 0.f};
+        x[2 * u + 1] =
+            sp < splits ? *(const f32x4*)(src + sp * step + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
     }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int s = s0 + 4 * u;
-      const float wu = __shfl(w, s < splits ? s : 0, 64);
-      const float ww = s < splits ? wu : 0.0f;
+    for (int u = 0; u < kWaveBatch; ++u) {
+      const int sp = s0 + u;
+      const float wu = __shfl(w, sp < splits ? sp : 0, 64);
+      const float ww = sp < splits ? wu : 0.0f;
       a0 += ww * x[2 * u];
       a1 += ww * x[2 * u + 1];
     }
   }
-  part[wave][0][lane] = a0;
-  part[wave][1][lane] = a1;
-  __syncthreads();
-  if (wave == 0) {
-    float lse_out = -INFINITY;
-    f32x4 r0 = {0.f, 0.f, 0.f, 0.f}, r1 = {0.f, 0.f, 0.f, 0.f};
-    if (mz != -INFINITY) {
-      const float zt = z + exp2f(sink2 - mz);
-      const float inv = 1.0f / zt;
-      r0 = (part[0][0][lane] + part[1][0][lane] + part[2][0][lane] + part[3][0][lane]) * inv;
-      r1 = (part[0][1][lane] + part[1][1][lane] + part[2][1][lane] + part[3][1][lane]) * inv;
-      lse_out = (mz + log2f(zt)) * kLn2;
-    }
-    *(u32x4*)(out + row * kHeadDim + 8 * lane) =
-        u32x4{bf16_rne(r0[0]) | (bf16_rne(r0[1]) << 16), bf16_rne(r0[2]) | (bf16_rne(r0[3]) << 16),
-              bf16_rne(r1[0]) | (bf16_rne(r1[1]) << 16), bf16_rne(r1[2]) | (bf16_rne(r1[3]) << 16)};
-    if (lane == 0) lse[row] = lse_out;
+  float lse_out = -INFINITY;
+  f32x4 r0 = {0.f, 0.f, 0.f, 0.f}, r1 = {0.f, 0.f, 0.f, 0.f};
+  if (mz != -INFINITY) {
+    const float zt = z + exp2f(sink2 - mz);
+    const float inv = 1.0f / zt;
+    r0 = a0 * inv;
+    r1 = a1 * inv;
+    lse_out = (mz + log2f(zt)) * kLn2;
   }
+  *(u32x4*)(out + row * kHeadDim + 8 * lane) =
+      u32x4{bf16_rne(r0[0]) | (bf16_rne(r0[1]) << 16), bf16_rne(r0[2]) | (bf16_rne(r0[3]) << 16),
+            bf16_rne(r1[0]) | (bf16_rne(r1[1]) << 16), bf16_rne(r1[2]) | (bf16_rne(r1[3]) << 16)};
+  if (lane == 0) lse[row] = lse_out;
 }
 
 // Merge split partials with the sink, for few rows (small batches). One
@@ -1001,8 +1004,8 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
       hipLaunchKernelGGL(combine_kernel, dim3((unsigned)(rows * kCombineSlices)), dim3(256), 0, s,
                          a.ws_o, a.ws_lse, sink, (int)slots, heads, out, lse);
     else
-      hipLaunchKernelGGL(combine_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, a.ws_o,
-                         a.ws_lse, sink, (int)slots, heads, out, lse);
+      hipLaunchKernelGGL(combine_wave_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s,
+                         a.ws_o, a.ws_lse, sink, (int)slots, heads, rows, out, lse);
     if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   }
   return RM_OK;
