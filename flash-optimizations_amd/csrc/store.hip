@@ -111,27 +111,79 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
-// Keep mask (bit i = coordinate 8*lane + i) of the kK largest magnitudes.
-// Bit-serial radix select of the kK-th largest key, fully unrolled: every step
-// compares the 8 keys of each lane against prefix|bit (one ballot per key slot,
-// popcounts on the scalar unit). `at` is the count at the last accepted step,
-// i.e. #{key >= threshold}; only when it exceeds kK is there a boundary tie
-// to admit in coordinate order.
-template <bool kBf16, int kK>
-__device__ __forceinline__ uint32_t select_top(const uint32_t* key) {
-  constexpr int kLow = kBf16 ? 16 : 0;  // bf16 magnitudes have zero low halves
-  uint32_t prefix = 0;
-  int at = 512;
+// #{key >= c} over the wave's 512 keys (one ballot per key slot, popcounts
+// on the scalar unit).
+__device__ __forceinline__ int count_ge(const uint32_t* key, uint32_t c) {
+  int cnt = 0;
 #pragma unroll
-  for (int b = 30; b >= kLow; --b) {
+  for (int i = 0; i < 8; ++i) cnt += popc_ballot(key[i] >= c);
+  return cnt;
+}
+
+// Bit-serial radix select of the kK-th largest key below an established
+// prefix: bits kTop..kLow, fully unrolled. `prefix` holds the threshold's bits
+// above kTop and `at` = #{key >= prefix}; on return `prefix` is the threshold
+// and `at` the count at the last accepted step.
+template <int kTop, int kLow, int kK>
+__device__ __forceinline__ void radix_bits(const uint32_t* key, uint32_t& prefix, int& at) {
+#pragma unroll
+  for (int b = kTop; b >= kLow; --b) {
     const uint32_t cand = prefix | (1u << b);
-    int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) cnt += popc_ballot(key[i] >= cand);
+    const int cnt = count_ge(key, cand);
     const bool take = cnt >= kK;
     prefix = take ? cand : prefix;
     at = take ? cnt : at;
   }
+}
+
+// Keep mask (bit i = coordinate 8*lane + i) of the kK largest magnitudes.
+// The threshold (the kK-th largest key) is found exponent first: the previous
+// record's threshold exponent `hint` and its neighbours are tried with two or
+// three counts (consecutive records of a layer have thresholds within a
+// binade or two), then the mantissa bits are resolved bit-serially; when the
+// exponent is not among them the search runs over all bits from bit 30. Both
+// ways give the same threshold. `at` is the count at the last accepted step,
+// i.e. #{key >= threshold}; only when it exceeds kK is there a boundary tie to
+// admit in coordinate order.
+template <bool kBf16, int kK>
+__device__ __forceinline__ uint32_t select_top(const uint32_t* key, uint32_t& hint) {
+  constexpr int kLow = kBf16 ? 16 : 0;  // bf16 magnitudes have zero low halves
+  const uint32_t e = hint;              // 1 <= e <= 252
+  uint32_t prefix = 0;
+  int at = 512;
+  bool found = false;
+  const int c_e = count_ge(key, e << 23);
+  if (c_e >= kK) {
+    const int c_up = count_ge(key, (e + 1) << 23);
+    if (c_up < kK) {
+      prefix = e << 23;
+      at = c_e;
+      found = true;
+    } else {
+      const int c_up2 = count_ge(key, (e + 2) << 23);
+      if (c_up2 < kK) {
+        prefix = (e + 1) << 23;
+        at = c_up;
+        found = true;
+      }
+    }
+  } else {
+    const int c_dn = count_ge(key, (e - 1) << 23);
+    if (c_dn >= kK) {
+      prefix = (e - 1) << 23;
+      at = c_dn;
+      found = true;
+    }
+  }
+  if (found) {
+    radix_bits<22, kLow, kK>(key, prefix, at);
+  } else {
+    prefix = 0;
+    at = 512;
+    radix_bits<30, kLow, kK>(key, prefix, at);
+  }
+  const uint32_t te = prefix >> 23;
+  hint = te < 1 ? 1u : (te > 252 ? 252u : te);
   uint32_t keep = 0;
   if (at == kK) {
 #pragma unroll
@@ -175,6 +227,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
       w[4 + i] = b[i];
     }
   }
+  uint32_t hint = 126;  // threshold exponent of this wave's previous record (|x| ~ 2^-1)
   for (int64_t rec = (int64_t)blockIdx.x * kWaves + wave; rec < n;
        rec += (int64_t)gridDim.x * kWaves) {
     const int64_t slot = slots[rec];
@@ -184,7 +237,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     load_row8<kBf16>(x, rec, stride, lane, v);
 #pragma unroll
     for (int i = 0; i < 8; ++i) key[i] = f2u(v[i]) & 0x7fffffffu;
-    const uint32_t keep = select_top<kBf16, kK>(key);
+    const uint32_t keep = select_top<kBf16, kK>(key, hint);
 
     // masked RMSNorm
     float m[8];
@@ -212,10 +265,13 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     // group amax: rounding is monotonic, so max |bf16(y)| = bf16(max |y|)
     float ay = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
     ay = fmaxf(ay, fmaxf(fmaxf(fabsf(y[4]), fabsf(y[5])), fmaxf(fabsf(y[6]), fabsf(y[7]))));
-    ay = fmaxf(ay, dpp<kDppXor1>(ay));  // max over the 8 lanes of the group
-    ay = fmaxf(ay, dpp<kDppXor2>(ay));
-    ay = fmaxf(ay, dpp<kDppHalfMirror>(ay));
-    const float amax = (float)(__bf16)ay;
+    // max over the 8 lanes of the group, on the bit patterns (ay >= 0, so
+    // integer order is float order): one DPP max per level
+    int ai = __float_as_int(ay);
+    ai = max(ai, __builtin_amdgcn_update_dpp(0, ai, kDppXor1, 0xf, 0xf, false));
+    ai = max(ai, __builtin_amdgcn_update_dpp(0, ai, kDppXor2, 0xf, 0xf, false));
+    ai = max(ai, __builtin_amdgcn_update_dpp(0, ai, kDppHalfMirror, 0xf, 0xf, false));
+    const float amax = (float)(__bf16)__int_as_float(ai);
     const int e = ue8m0_exponent(amax);
 
     // E4M3 codes = RNE(n / 2^e) by the scaled hardware conversion (identical to
