@@ -85,6 +85,35 @@ def test_pack_bit_exact_tie_rows():
                           oracle_pack(x.to(dtype), slots, 1))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_pack_bit_exact_many_records_per_wave_mixed_scales(dtype):
+    """300,000 records: every wave packs about nine (records 32,768 apart), so
+    the threshold search starts from the previous record's exponent. A wave's
+    records share a scale up to a factor of 2^(+-1) (the guess, its upper and
+    its lower neighbour), every seventh record jumps by up to 2^30 (a miss);
+    zero and tie rows are mixed in. 6,000 records spread over the pool are
+    checked byte for byte."""
+    banner(f"pack 300000 records mixed scales {dtype}")
+    n = 300000
+    g = torch.Generator().manual_seed(46)
+    x = syn.latents(n, seed=46).float()
+    wave_scale = torch.randint(-30, 31, (32768,), generator=g)
+    k = wave_scale[torch.arange(n) % 32768] + torch.randint(-1, 2, (n,), generator=g)
+    jump = torch.arange(n) % 7 == 3
+    k[jump] = torch.randint(-30, 31, (int(jump.sum()),), generator=g)
+    x = x * torch.pow(2.0, k.float())[:, None]
+    x[::997] = 0.0
+    x[5::1999] = torch.arange(512, dtype=torch.float32) % 7
+    slots = np.random.default_rng(46).permutation(n).astype(np.int32)
+    pages = n // 64 + 1
+    gpu = gpu_pack(x.to(dtype), slots, pages)
+    pick = np.random.default_rng(47).choice(n, 6000, replace=False)
+    ref = oracle_pack(x[pick].to(dtype), slots[pick], pages)
+    got = gpu.layer().cpu().numpy().reshape(-1, 328)
+    want = ref.reshape(-1, 328)
+    assert np.array_equal(got[slots[pick]], want[slots[pick]])
+
+
 def test_pack_skips_out_of_range_slots_and_leaves_canaries():
     banner("pack invalid slots")
     x = syn.latents(128, seed=5)
