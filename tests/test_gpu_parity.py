@@ -677,6 +677,17 @@ def test_decode_swa_reference_shape_h64_b16():
     check_decode(c)
 
 
+def test_decode_swa_reference_shape_h128_b16_two_head_groups():
+    """The reference's H128/B16/top-k 512 decode with 64 window rows: 128
+    token x 16-head blocks, so 32-head workgroups (two groups per expanded
+    record) read both the C4 splits and the window split."""
+    banner("decode swa H=128 B=16 topk=512")
+    ctx = syn.log_uniform_contexts(16, 2048, 16384, 39)
+    c = build_decode_case(ctx, q_len=1, heads=128, topk=512, seed=39)
+    add_swa(c, 64, seed=40)
+    check_decode(c)
+
+
 def test_decode_swa_only_and_window_128_next_n2():
     """Empty C4 selections (only the window and the sink remain) and a
     128-row window with two query tokens per request."""
