@@ -215,6 +215,23 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     int64_t pool_rows) {
   using R = Rec<kK>;
   __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][R::kSpill + 64];
+  // compaction selectors: for a keep byte, byte p of the entry is the slot
+  // (0..7) of its p-th survivor, or 0x0c (a zero byte) past the last one
+  __shared__ uint64_t ctab[256];
+  {
+    const uint32_t k = threadIdx.x;  // 256 threads: one entry each
+    uint64_t sel = 0x0c0c0c0c0c0c0c0cull;
+    int p = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if ((k >> i) & 1u) {
+        sel = (sel & ~(0xffull << (8 * p))) | ((uint64_t)i << (8 * p));
+        ++p;
+      }
+    }
+    ctab[k] = sel;
+  }
+  __syncthreads();
   const int lane = wave_lane();
   const int wave = uniform((int)(threadIdx.x >> 6));
   uint8_t* st = stage[wave];
@@ -239,10 +256,11 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     for (int i = 0; i < 8; ++i) key[i] = f2u(v[i]) & 0x7fffffffu;
     const uint32_t keep = select_top<kBf16, kK>(key, hint);
 
-    // masked RMSNorm
+    // masked RMSNorm (pruned values cleared with a sign-extended keep bit)
     float m[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) m[i] = (keep >> i) & 1u ? v[i] : 0.0f;
+    for (int i = 0; i < 8; ++i)
+      m[i] = __int_as_float(__float_as_int(v[i]) & __builtin_amdgcn_sbfe((int)keep, i, 1));
     float p = m[0] * m[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) {
@@ -285,18 +303,21 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     const uint32_t lo = __builtin_bit_cast(uint32_t, c01), hi = __builtin_bit_cast(uint32_t, c45);
 
     // compaction: survivors go to [rank, rank + popcount) in coordinate order,
-    // rank = survivors in lower lanes (a wave prefix sum); pruned codes go to a
-    // per-lane spill byte past the record, so the stores are unconditional
+    // rank = survivors in lower lanes (a wave prefix sum). v_perm packs the
+    // lane's surviving codes into the low bytes of 8 (zeros above), which are
+    // OR-ed into the zeroed code area at byte offset rank: two 8-byte LDS ORs
+    // at the aligned words the run touches (neighbouring lanes share words).
     const int cnt = __popc(keep);
-    uint8_t* const base = st + wave_exclusive_sum(cnt);
-    uint8_t* const spill = st + R::kSpill + lane;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const bool kept = (keep >> i) & 1u;
-      const uint32_t below = keep & ((1u << i) - 1u);  // survivors before slot i
-      uint8_t* const at = kept ? base + __popc(below) : spill;
-      *at = (uint8_t)((i < 4 ? lo : hi) >> (8 * (i & 3)));
-    }
+    const int rank = wave_exclusive_sum(cnt);
+    if (lane < kK / 8) *(uint64_t*)(st + 8 * lane) = 0;
+    const uint64_t sel = ctab[keep];
+    const uint64_t run = ((uint64_t)__builtin_amdgcn_perm(hi, lo, (uint32_t)(sel >> 32)) << 32) |
+                         __builtin_amdgcn_perm(hi, lo, (uint32_t)sel);
+    const uint32_t sh = 8u * (uint32_t)(rank & 7);
+    uint64_t* const word = (uint64_t*)(st + (rank & ~7));
+    __hip_atomic_fetch_or(word, run << sh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+    __hip_atomic_fetch_or(word + 1, (run >> 1) >> (63u - sh), __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_WAVEFRONT);
     // bitmap byte: coordinate 8l+i is bit 7-i of byte 7 - l%8 of word l/8
     const uint32_t rev = __builtin_bitreverse32(keep) >> 24;
     st[kK + 8 * (lane >> 3) + 7 - (lane & 7)] = (uint8_t)rev;
