@@ -92,9 +92,9 @@ __device__ __forceinline__ int popc_ballot(bool pred) {
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 
-// Exclusive prefix sum of x over the wave's lanes (row shifts within rows of 16,
-// then row broadcasts 15 and 31).
-__device__ __forceinline__ int wave_exclusive_sum(int x) {
+// Inclusive prefix sum of x over the wave's lanes (row shifts within rows of
+// 16, then row broadcasts 15 and 31); the exclusive sum subtracts x.
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
   int v = x;
   v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
   v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
@@ -102,8 +102,9 @@ __device__ __forceinline__ int wave_exclusive_sum(int x) {
   v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
   v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false); // row_bcast:15
   v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false); // row_bcast:31
-  return v - x;
+  return v;
 }
+__device__ __forceinline__ int wave_exclusive_sum(int x) { return wave_inclusive_sum(x) - x; }
 
 // Exclusive count of set predicates in lanes below this one.
 __device__ __forceinline__ int lanes_below(uint64_t mask) {
@@ -136,53 +137,92 @@ __device__ __forceinline__ void radix_bits(const uint32_t* key, uint32_t& prefix
   }
 }
 
+// Mantissa bits 22..16 of the threshold inside its binade [E, E + 1), from a
+// histogram of the binade's keys instead of seven bit-serial counts. `above` =
+// #{key >= (E + 1) << 23} < kK <= #{key >= E << 23}. The wave's 128 LDS bins
+// (zero on entry, zero again on return) count the binade's keys by those
+// seven bits; lane l reads bins 127 - 2l and 126 - 2l, so an inclusive scan
+// over the lanes gives S(m) = #{binade keys with bits >= m}, and the threshold
+// bits are the largest m with above + S(m) >= kK. On return `prefix` holds
+// E and those bits and `at` = #{key >= prefix}, as the bit-serial search
+// leaves them.
+template <int kK>
+__device__ __forceinline__ void binade_histogram(const uint32_t* key, uint32_t e, int above,
+                                                 uint32_t* hist, uint32_t& prefix, int& at) {
+  const uint32_t base = e << 23;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t idx = key[i] - base;
+    if (idx < (1u << 23))
+      __hip_atomic_fetch_add(hist + (idx >> 16), 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WAVEFRONT);
+  }
+  wave_lds_sync();
+  const int lane = wave_lane();
+  uint64_t* const pair = (uint64_t*)(hist + 126 - 2 * lane);
+  const uint64_t h = *pair;
+  *pair = 0;  // in order after the read: the bins are clear for the next record
+  const int lo = (int)(uint32_t)h, hi = (int)(uint32_t)(h >> 32);
+  const int incl = wave_inclusive_sum(lo + hi);  // S(126 - 2 lane)
+  const int need = kK - above;                   // >= 1, and S(0) >= need
+  const int l = (int)__builtin_ctzll(__ballot(incl >= need));
+  const int s_lo = __builtin_amdgcn_readlane(incl, l);         // S(126 - 2l)
+  const int s_hi = s_lo - __builtin_amdgcn_readlane(lo, l);    // S(127 - 2l)
+  const bool upper = s_hi >= need;
+  prefix = base | ((uint32_t)(upper ? 127 - 2 * l : 126 - 2 * l) << 16);
+  at = above + (upper ? s_hi : s_lo);
+}
+
 // Keep mask (bit i = coordinate 8*lane + i) of the kK largest magnitudes.
 // The threshold (the kK-th largest key) is found exponent first: the previous
 // record's threshold exponent `hint` and its neighbours are tried with two or
 // three counts (consecutive records of a layer have thresholds within a
-// binade or two), then the mantissa bits are resolved bit-serially; when the
-// exponent is not among them the search runs over all bits from bit 30. Both
+// binade or two), then mantissa bits 22..16 come from a histogram of that
+// binade (and, for FP32 keys, bits 15..0 bit-serially); when the exponent is
+// not among them the search runs bit-serially over all bits from bit 30. Both
 // ways give the same threshold. `at` is the count at the last accepted step,
 // i.e. #{key >= threshold}; only when it exceeds kK is there a boundary tie to
 // admit in coordinate order.
 template <bool kBf16, int kK>
-__device__ __forceinline__ uint32_t select_top(const uint32_t* key, uint32_t& hint) {
+__device__ __forceinline__ uint32_t select_top(const uint32_t* key, uint32_t& hint,
+                                               uint32_t* hist) {
   constexpr int kLow = kBf16 ? 16 : 0;  // bf16 magnitudes have zero low halves
   const uint32_t e = hint;              // 1 <= e <= 252
-  uint32_t prefix = 0;
-  int at = 512;
+  uint32_t prefix = 0, te = 0;
+  int at = 512, above = 0;
   bool found = false;
   const int c_e = count_ge(key, e << 23);
   if (c_e >= kK) {
     const int c_up = count_ge(key, (e + 1) << 23);
     if (c_up < kK) {
-      prefix = e << 23;
-      at = c_e;
+      te = e;
+      above = c_up;
       found = true;
     } else {
       const int c_up2 = count_ge(key, (e + 2) << 23);
       if (c_up2 < kK) {
-        prefix = (e + 1) << 23;
-        at = c_up;
+        te = e + 1;
+        above = c_up2;
         found = true;
       }
     }
   } else {
     const int c_dn = count_ge(key, (e - 1) << 23);
     if (c_dn >= kK) {
-      prefix = (e - 1) << 23;
-      at = c_dn;
+      te = e - 1;
+      above = c_e;
       found = true;
     }
   }
   if (found) {
-    radix_bits<22, kLow, kK>(key, prefix, at);
+    binade_histogram<kK>(key, te, above, hist, prefix, at);
+    if (!kBf16) radix_bits<15, 0, kK>(key, prefix, at);
   } else {
     prefix = 0;
     at = 512;
     radix_bits<30, kLow, kK>(key, prefix, at);
   }
-  const uint32_t te = prefix >> 23;
+  te = prefix >> 23;
   hint = te < 1 ? 1u : (te > 252 ? 252u : te);
   uint32_t keep = 0;
   if (at == kK) {
@@ -218,6 +258,11 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
   // compaction selectors: for a keep byte, byte p of the entry is the slot
   // (0..7) of its p-th survivor, or 0x0c (a zero byte) past the last one
   __shared__ uint64_t ctab[256];
+  // per-wave histogram bins of the threshold binade's mantissas (kept zero
+  // between records)
+  __shared__ __attribute__((aligned(16))) uint32_t bins[kWaves][128];
+  bins[threadIdx.x >> 6][2 * (threadIdx.x & 63)] = 0;
+  bins[threadIdx.x >> 6][2 * (threadIdx.x & 63) + 1] = 0;
   {
     const uint32_t k = threadIdx.x;  // 256 threads: one entry each
     uint64_t sel = 0x0c0c0c0c0c0c0c0cull;
@@ -254,7 +299,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     load_row8<kBf16>(x, rec, stride, lane, v);
 #pragma unroll
     for (int i = 0; i < 8; ++i) key[i] = f2u(v[i]) & 0x7fffffffu;
-    const uint32_t keep = select_top<kBf16, kK>(key, hint);
+    const uint32_t keep = select_top<kBf16, kK>(key, hint, bins[wave]);
 
     // masked RMSNorm (pruned values cleared with a sign-extended keep bit)
     float m[8];
