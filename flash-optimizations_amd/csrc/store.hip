@@ -56,6 +56,41 @@ __device__ __forceinline__ void load_row8(const void* x, int64_t row, int64_t st
   }
 }
 
+// The lane's raw slice of a row (BF16: one 16-byte load; FP32: two), loaded
+// one record ahead of its use so the load latency overlaps the previous
+// record's work.
+struct RowRaw {
+  u32x4 a, b;
+};
+
+template <bool kBf16>
+__device__ __forceinline__ RowRaw load_raw(const void* x, int64_t row, int64_t stride, int lane) {
+  RowRaw r;
+  if (kBf16) {
+    r.a = *(const u32x4*)((const uint16_t*)x + row * stride + 8 * lane);
+    r.b = r.a;
+  } else {
+    const float* p = (const float*)x + row * stride + 8 * lane;
+    r.a = *(const u32x4*)p;
+    r.b = *(const u32x4*)(p + 4);
+  }
+  return r;
+}
+
+template <bool kBf16>
+__device__ __forceinline__ void unpack_raw(const RowRaw& r, float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (kBf16) {
+      v[2 * i] = u2f(r.a[i] << 16);
+      v[2 * i + 1] = u2f(r.a[i] & 0xffff0000u);
+    } else {
+      v[i] = u2f(r.a[i]);
+      v[4 + i] = u2f(r.b[i]);
+    }
+  }
+}
+
 // Lane exchanges within rows of 16 (DPP): xor 1 and xor 2 inside quads, then
 // the mirrors, which pair each lane with one in the other half of its group of
 // 8 (16). In a butterfly reduction every lane of an aligned group already holds
@@ -290,13 +325,26 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     }
   }
   uint32_t hint = 126;  // threshold exponent of this wave's previous record (|x| ~ 2^-1)
-  for (int64_t rec = (int64_t)blockIdx.x * kWaves + wave; rec < n;
-       rec += (int64_t)gridDim.x * kWaves) {
-    const int64_t slot = slots[rec];
+  const int64_t step = (int64_t)gridDim.x * kWaves;
+  int64_t rec = (int64_t)blockIdx.x * kWaves + wave;
+  RowRaw cur{};
+  int32_t cur_slot = -1;
+  if (rec < n) {
+    cur = load_raw<kBf16>(x, rec, stride, lane);
+    cur_slot = slots[rec];
+  }
+  for (; rec < n; rec += step) {
+    // the next record's row and slot are in flight while this one is packed
+    const RowRaw raw = cur;
+    const int32_t slot = cur_slot;
+    if (rec + step < n) {
+      cur = load_raw<kBf16>(x, rec + step, stride, lane);
+      cur_slot = slots[rec + step];
+    }
     if (slot < 0 || slot >= pool_rows) continue;
     float v[8];
     uint32_t key[8];
-    load_row8<kBf16>(x, rec, stride, lane, v);
+    unpack_raw<kBf16>(raw, v);
 #pragma unroll
     for (int i = 0; i < 8; ++i) key[i] = f2u(v[i]) & 0x7fffffffu;
     const uint32_t keep = select_top<kBf16, kK>(key, hint, bins[wave]);
@@ -371,7 +419,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
 
     // the record is 8-byte aligned: one 8-byte store per lane (41 lanes for the
     // 328-byte record; the 520-byte 448-survivor record needs a 65th piece)
-    uint8_t* dst = pool + (slot >> 6) * R::kPage + (slot & 63) * R::kBytes;
+    uint8_t* dst = pool + (int64_t)(slot >> 6) * R::kPage + (slot & 63) * R::kBytes;
     if (lane < R::kPieces) *(u32x2*)(dst + 8 * lane) = *(const u32x2*)(st + 8 * lane);
     if (R::kPieces > 64 && lane < R::kPieces - 64)
       *(u32x2*)(dst + 512 + 8 * lane) = *(const u32x2*)(st + 512 + 8 * lane);
