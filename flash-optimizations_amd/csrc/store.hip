@@ -116,8 +116,11 @@ __device__ __forceinline__ float wave_tree_sum(float p) {
   p = p + dpp<kDppXor2>(p);
   p = p + dpp<kDppHalfMirror>(p);
   p = p + dpp<kDppMirror>(p);
-  // rows of 16 are now uniform: levels 16 and 32 give (r0 + r1) + (r2 + r3)
-  return (lane_value(p, 0) + lane_value(p, 16)) + (lane_value(p, 32) + lane_value(p, 48));
+  // rows of 16 are now uniform (r0..r3): row broadcast 15 gives rows 1 and 3
+  // r0 + r1 and r2 + r3, row broadcast 31 gives row 3 (r0 + r1) + (r2 + r3)
+  p = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(p), 0x142, 0xa, 0xf, false)) + p;
+  p = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(p), 0x143, 0xc, 0xf, false)) + p;
+  return lane_value(p, 63);
 }
 
 __device__ __forceinline__ int popc_ballot(bool pred) {
@@ -180,10 +183,12 @@ __device__ __forceinline__ void radix_bits(const uint32_t* key, uint32_t& prefix
 // over the lanes gives S(m) = #{binade keys with bits >= m}, and the threshold
 // bits are the largest m with above + S(m) >= kK. On return `prefix` holds
 // E and those bits and `at` = #{key >= prefix}, as the bit-serial search
-// leaves them.
+// leaves them; `tied` = the threshold bin's count (for BF16 keys, the keys
+// equal to the threshold).
 template <int kK>
 __device__ __forceinline__ void binade_histogram(const uint32_t* key, uint32_t e, int above,
-                                                 uint32_t* hist, uint32_t& prefix, int& at) {
+                                                 uint32_t* hist, uint32_t& prefix, int& at,
+                                                 int& tied) {
   const uint32_t base = e << 23;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -206,6 +211,56 @@ __device__ __forceinline__ void binade_histogram(const uint32_t* key, uint32_t e
   const bool upper = s_hi >= need;
   prefix = base | ((uint32_t)(upper ? 127 - 2 * l : 126 - 2 * l) << 16);
   at = above + (upper ? s_hi : s_lo);
+  tied = upper ? __builtin_amdgcn_readlane(hi, l) : __builtin_amdgcn_readlane(lo, l);
+}
+
+// Masked values: m[i] = v[i] where bit i of `keep` is set, else 0.
+__device__ __forceinline__ void mask_by_keep(const float* v, uint32_t keep, float* m) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    m[i] = __int_as_float(__float_as_int(v[i]) & __builtin_amdgcn_sbfe((int)keep, i, 1));
+}
+
+// Keep mask for BF16 keys at threshold t with at = #{key >= t} and tied =
+// #{key == t}: every key above t, and the (kK - (at - tied)) lowest-coordinate
+// keys equal to t; m receives the kept values. Keys and t are below 2^31, so
+// key < t is the borrow (and the sign) of key - t, which also clears the
+// pruned value, and key > t is the sign of t - key; the sign bits are shifted
+// into the byte by a funnel shift, slot 7 first. Ties are ranked by a wave
+// prefix sum of each lane's tie count; a lane keeps its first `admit` ties,
+// cut at the position of its admit-th tie (byte `admit` of the selector table
+// entry of its tie byte).
+template <int kK>
+__device__ __forceinline__ uint32_t keep_at_threshold(const uint32_t* key, const float* v,
+                                                      float* m, uint32_t t, int at, int tied,
+                                                      const uint64_t* ctab) {
+  uint32_t lt = 0;
+  bool below[8];
+#pragma unroll
+  for (int i = 7; i >= 0; --i) {
+    uint32_t borrow;
+    const uint32_t x = __builtin_subc(key[i], t, 0u, &borrow);
+    lt = __builtin_amdgcn_alignbit(lt, x, 31);
+    below[i] = borrow != 0;
+  }
+  const uint32_t ge = ~lt & 0xffu;
+  if (at == kK) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m[i] = below[i] ? 0.0f : v[i];
+    return ge;
+  }
+  uint32_t gt = 0;
+#pragma unroll
+  for (int i = 7; i >= 0; --i) gt = __builtin_amdgcn_alignbit(gt, t - key[i], 31);
+  gt &= 0xffu;
+  const uint32_t tie = ge & ~gt;
+  const int need = kK - (at - tied);  // ties to admit: 1 <= need < tied
+  const int cnt = __popc(tie);
+  const int admit = min(max(need - wave_exclusive_sum(cnt), 0), cnt);
+  const uint32_t cut = (uint32_t)(ctab[tie] >> (8 * (admit & 7))) & 7u;
+  const uint32_t keep = gt | (admit < cnt ? tie & ((1u << cut) - 1u) : tie);
+  mask_by_keep(v, keep, m);
+  return keep;
 }
 
 // Keep mask (bit i = coordinate 8*lane + i) of the kK largest magnitudes.
@@ -219,8 +274,9 @@ __device__ __forceinline__ void binade_histogram(const uint32_t* key, uint32_t e
 // i.e. #{key >= threshold}; only when it exceeds kK is there a boundary tie to
 // admit in coordinate order.
 template <bool kBf16, int kK>
-__device__ __forceinline__ uint32_t select_top(const uint32_t* key, uint32_t& hint,
-                                               uint32_t* hist) {
+__device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float* v, float* m,
+                                               uint32_t& hint, uint32_t* hist,
+                                               const uint64_t* ctab) {
   constexpr int kLow = kBf16 ? 16 : 0;  // bf16 magnitudes have zero low halves
   const uint32_t e = hint;              // 1 <= e <= 252
   uint32_t prefix = 0, te = 0;
@@ -250,8 +306,13 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, uint32_t& hi
     }
   }
   if (found) {
-    binade_histogram<kK>(key, te, above, hist, prefix, at);
-    if (!kBf16) radix_bits<15, 0, kK>(key, prefix, at);
+    int tied;
+    binade_histogram<kK>(key, te, above, hist, prefix, at, tied);
+    if (kBf16) {
+      hint = te < 1 ? 1u : (te > 252 ? 252u : te);
+      return keep_at_threshold<kK>(key, v, m, prefix, at, tied, ctab);
+    }
+    radix_bits<15, 0, kK>(key, prefix, at);
   } else {
     prefix = 0;
     at = 512;
@@ -263,6 +324,7 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, uint32_t& hi
   if (at == kK) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) keep |= (key[i] >= prefix ? 1u : 0u) << i;
+    mask_by_keep(v, keep, m);
     return keep;
   }
   // admit the (kK - #{key > prefix}) lowest-coordinate ties at the threshold
@@ -280,6 +342,7 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, uint32_t& hi
     before += tie ? 1 : 0;
     keep |= (k ? 1u : 0u) << i;
   }
+  mask_by_keep(v, keep, m);
   return keep;
 }
 
@@ -347,13 +410,11 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     unpack_raw<kBf16>(raw, v);
 #pragma unroll
     for (int i = 0; i < 8; ++i) key[i] = f2u(v[i]) & 0x7fffffffu;
-    const uint32_t keep = select_top<kBf16, kK>(key, hint, bins[wave]);
-
-    // masked RMSNorm (pruned values cleared with a sign-extended keep bit)
+    // keep mask and the kept values m (pruned values cleared)
     float m[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      m[i] = __int_as_float(__float_as_int(v[i]) & __builtin_amdgcn_sbfe((int)keep, i, 1));
+    const uint32_t keep = select_top<kBf16, kK>(key, v, m, hint, bins[wave], ctab);
+
+    // masked RMSNorm
     float p = m[0] * m[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) {
