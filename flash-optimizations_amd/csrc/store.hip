@@ -123,6 +123,23 @@ __device__ __forceinline__ float wave_tree_sum(float p) {
   return lane_value(p, 63);
 }
 
+// r = RN(1 / RN(sqrt(sumsq / 512 + eps))) for the wave-uniform sum. For
+// 2^-96 <= x < 2^128 the root s lies in [2^-48, 2^64), where v_sqrt_f32 is
+// the correctly rounded root (the compiler's __fsqrt_rn applies no scaling
+// there) and one Newton step from v_rcp_f32, fma(fma(-s, r0, 1), r0, r0),
+// equals __fdiv_rn(1, s) for every float s (checked exhaustively on gfx950
+// for all s in that range); other x take the general sequence.
+__device__ __forceinline__ float inv_rms(float sumsq, float eps) {
+  const float x = sumsq * (1.0f / 512.0f) + eps;
+  const uint32_t xb = (uint32_t)__builtin_amdgcn_readfirstlane(__float_as_int(x));
+  if (xb - 0x0f800000u < 0x7f800000u - 0x0f800000u) {
+    const float s = __builtin_amdgcn_sqrtf(__uint_as_float(xb));
+    const float r0 = __builtin_amdgcn_rcpf(s);
+    return __builtin_fmaf(__builtin_fmaf(-s, r0, 1.0f), r0, r0);
+  }
+  return __fdiv_rn(1.0f, __fsqrt_rn(__uint_as_float(xb)));
+}
+
 __device__ __forceinline__ int popc_ballot(bool pred) {
   return __popcll(__ballot(pred));
 }
@@ -422,7 +439,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
       p = p + sq;
     }
     const float sumsq = wave_tree_sum(p);
-    const float r = __fdiv_rn(1.0f, __fsqrt_rn(sumsq * (1.0f / 512.0f) + eps));
+    const float r = inv_rms(sumsq, eps);
     // n = bf16(RN(RN(m * r) * w)) with the hardware round-to-nearest-even
     // conversion (identical to the software rounding for every non-NaN input)
     float y[8];
@@ -517,7 +534,7 @@ __global__ __launch_bounds__(256) void native_store_kernel(
       p = p + sq;
     }
     const float sumsq = wave_tree_sum(p);
-    const float r = __fdiv_rn(1.0f, __fsqrt_rn(sumsq * (1.0f / 512.0f) + eps));
+    const float r = inv_rms(sumsq, eps);
     float nf[8];
     float amax = 0.0f;
 #pragma unroll
