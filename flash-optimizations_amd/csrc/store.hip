@@ -192,26 +192,28 @@ __device__ __forceinline__ void radix_bits(const uint32_t* key, uint32_t& prefix
   }
 }
 
-// Mantissa bits 22..16 of the threshold inside its binade [E, E + 1), from a
-// histogram of the binade's keys instead of seven bit-serial counts. `above` =
-// #{key >= (E + 1) << 23} < kK <= #{key >= E << 23}. The wave's 128 LDS bins
-// (zero on entry, zero again on return) count the binade's keys by those
+// The top seven mantissa bits of the threshold inside its binade [E, E + 1),
+// from a histogram of the binade's keys instead of seven bit-serial counts.
+// Keys hold the exponent from bit kExp up (BF16 keys: the 15-bit magnitude,
+// kExp = 7; FP32 keys: the 31-bit magnitude, kExp = 23). `above` =
+// #{key >= (E + 1) << kExp} < kK <= #{key >= E << kExp}. The wave's 128 LDS
+// bins (zero on entry, zero again on return) count the binade's keys by those
 // seven bits; lane l reads bins 127 - 2l and 126 - 2l, so an inclusive scan
 // over the lanes gives S(m) = #{binade keys with bits >= m}, and the threshold
 // bits are the largest m with above + S(m) >= kK. On return `prefix` holds
 // E and those bits and `at` = #{key >= prefix}, as the bit-serial search
 // leaves them; `tied` = the threshold bin's count (for BF16 keys, the keys
 // equal to the threshold).
-template <int kK>
+template <int kK, int kExp>
 __device__ __forceinline__ void binade_histogram(const uint32_t* key, uint32_t e, int above,
                                                  uint32_t* hist, uint32_t& prefix, int& at,
                                                  int& tied) {
-  const uint32_t base = e << 23;
+  const uint32_t base = e << kExp;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t idx = key[i] - base;
-    if (idx < (1u << 23))
-      __hip_atomic_fetch_add(hist + (idx >> 16), 1u, __ATOMIC_RELAXED,
+    if (idx < (1u << kExp))
+      __hip_atomic_fetch_add(hist + (idx >> (kExp - 7)), 1u, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_WAVEFRONT);
   }
   wave_lds_sync();
@@ -226,7 +228,7 @@ __device__ __forceinline__ void binade_histogram(const uint32_t* key, uint32_t e
   const int s_lo = __builtin_amdgcn_readlane(incl, l);         // S(126 - 2l)
   const int s_hi = s_lo - __builtin_amdgcn_readlane(lo, l);    // S(127 - 2l)
   const bool upper = s_hi >= need;
-  prefix = base | ((uint32_t)(upper ? 127 - 2 * l : 126 - 2 * l) << 16);
+  prefix = base | ((uint32_t)(upper ? 127 - 2 * l : 126 - 2 * l) << (kExp - 7));
   at = above + (upper ? s_hi : s_lo);
   tied = upper ? __builtin_amdgcn_readlane(hi, l) : __builtin_amdgcn_readlane(lo, l);
 }
@@ -286,7 +288,7 @@ __device__ __forceinline__ uint32_t keep_at_threshold(const uint32_t* key, const
 // three counts (consecutive records of a layer have thresholds within a
 // binade or two), then mantissa bits 22..16 come from a histogram of that
 // binade (and, for FP32 keys, bits 15..0 bit-serially); when the exponent is
-// not among them the search runs bit-serially over all bits from bit 30. Both
+// not among them the search runs bit-serially over all key bits. Both
 // ways give the same threshold. `at` is the count at the last accepted step,
 // i.e. #{key >= threshold}; only when it exceeds kK is there a boundary tie to
 // admit in coordinate order.
@@ -294,20 +296,20 @@ template <bool kBf16, int kK>
 __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float* v, float* m,
                                                uint32_t& hint, uint32_t* hist,
                                                const uint64_t* ctab) {
-  constexpr int kLow = kBf16 ? 16 : 0;  // bf16 magnitudes have zero low halves
+  constexpr int kExp = kBf16 ? 7 : 23;  // key bit of the exponent's LSB
   const uint32_t e = hint;              // 1 <= e <= 252
   uint32_t prefix = 0, te = 0;
   int at = 512, above = 0;
   bool found = false;
-  const int c_e = count_ge(key, e << 23);
+  const int c_e = count_ge(key, e << kExp);
   if (c_e >= kK) {
-    const int c_up = count_ge(key, (e + 1) << 23);
+    const int c_up = count_ge(key, (e + 1) << kExp);
     if (c_up < kK) {
       te = e;
       above = c_up;
       found = true;
     } else {
-      const int c_up2 = count_ge(key, (e + 2) << 23);
+      const int c_up2 = count_ge(key, (e + 2) << kExp);
       if (c_up2 < kK) {
         te = e + 1;
         above = c_up2;
@@ -315,7 +317,7 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
       }
     }
   } else {
-    const int c_dn = count_ge(key, (e - 1) << 23);
+    const int c_dn = count_ge(key, (e - 1) << kExp);
     if (c_dn >= kK) {
       te = e - 1;
       above = c_e;
@@ -324,7 +326,7 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
   }
   if (found) {
     int tied;
-    binade_histogram<kK>(key, te, above, hist, prefix, at, tied);
+    binade_histogram<kK, kExp>(key, te, above, hist, prefix, at, tied);
     if (kBf16) {
       hint = te < 1 ? 1u : (te > 252 ? 252u : te);
       return keep_at_threshold<kK>(key, v, m, prefix, at, tied, ctab);
@@ -333,9 +335,9 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
   } else {
     prefix = 0;
     at = 512;
-    radix_bits<30, kLow, kK>(key, prefix, at);
+    radix_bits<kExp + 7, 0, kK>(key, prefix, at);
   }
-  te = prefix >> 23;
+  te = prefix >> kExp;
   hint = te < 1 ? 1u : (te > 252 ? 252u : te);
   uint32_t keep = 0;
   if (at == kK) {
@@ -426,7 +428,8 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     uint32_t key[8];
     unpack_raw<kBf16>(raw, v);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) key[i] = f2u(v[i]) & 0x7fffffffu;
+    for (int i = 0; i < 8; ++i)  // BF16: the 15-bit magnitude; FP32: the 31-bit one
+      key[i] = kBf16 ? (raw.a[i / 2] >> (16 * (i & 1))) & 0x7fffu : f2u(v[i]) & 0x7fffffffu;
     // keep mask and the kept values m (pruned values cleared)
     float m[8];
     const uint32_t keep = select_top<kBf16, kK>(key, v, m, hint, bins[wave], ctab);
