@@ -58,6 +58,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--min-warmup-ms", type=float, default=250.0,
+                   help="continue the bulk leg's warmup steps for at least this long")
     p.add_argument("--records", type=int, default=1 << 20)
     p.add_argument("--quick", action="store_true", help="skip decode, capacity and CPU legs")
     p.add_argument("--no-capacity", action="store_true")
@@ -106,9 +108,17 @@ def bulk(torch, remnant, args):
     def recon_rope():
         remnant.unpack_gather_bf16(pool, physical, raw, lengths, freqs, out, fused_rope=True)
 
-    for _ in range(args.warmup):
+    # untimed warmup: at least args.warmup steps, continued until the GPU has
+    # run the step for args.min_warmup_ms of wall time, so the timed steps see
+    # the clocks of sustained load rather than the ramp out of idle
+    t_w = time.perf_counter()
+    done = 0
+    while done < args.warmup or (time.perf_counter() - t_w) * 1e3 < args.min_warmup_ms:
         pack()
         recon()
+        done += 1
+        if done % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     k = args.steps
     ev = events(torch, 3 * k)
@@ -135,7 +145,7 @@ def bulk(torch, remnant, args):
     torch.cuda.synchronize()
     rope_ms = e2[0].elapsed_time(e2[1]) / k
     return dict(n=n, steps=k, total_ms=total_ms, wall_ms=wall, pack_ms=pack_ms,
-                recon_ms=recon_ms, rope_ms=rope_ms)
+                recon_ms=recon_ms, rope_ms=rope_ms, warmup_run=done)
 
 
 def build_decode(torch, remnant, contexts, q_len, topk, packed, seed, pool_pages=None, heads=16,
@@ -484,6 +494,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": b["warmup_run"],
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
