@@ -114,6 +114,24 @@ def test_pack_bit_exact_many_records_per_wave_mixed_scales(dtype):
     assert np.array_equal(got[slots[pick]], want[slots[pick]])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("eps", [0.0, 1e-6], ids=["eps0", "eps1e-6"])
+def test_pack_bit_exact_rms_root_paths(dtype, eps):
+    """Row scales 2^-72 .. 2^66 put x = sum(m^2)/512 + eps below 2^-96 (the
+    general root and reciprocal, including subnormal squares), inside
+    [2^-96, 2^128) (v_sqrt_f32 and one Newton step from v_rcp_f32) and past
+    the FP32 range (an infinite sum), for both input types."""
+    banner(f"pack rms root paths {dtype} eps={eps}")
+    k = torch.tensor([-72, -70, -66, -62, -58, -55, -52, -50, -48, -47, -46, -40, -20, 0, 20,
+                      40, 50, 55, 58, 60, 62, 63, 64, 65, 66] * 3, dtype=torch.float32)
+    n = k.numel()
+    x = syn.latents(n, seed=48).float() * torch.pow(2.0, k)[:, None]
+    slots = np.arange(n, dtype=np.int32)
+    pages = (n + 63) // 64
+    assert_pool_equal(gpu_pack(x.to(dtype), slots, pages, eps=eps),
+                      oracle_pack(x.to(dtype), slots, pages, eps=eps))
+
+
 def test_pack_skips_out_of_range_slots_and_leaves_canaries():
     banner("pack invalid slots")
     x = syn.latents(128, seed=5)
