@@ -184,6 +184,11 @@ __device__ __forceinline__ void store_native(uint8_t* out, int64_t row, u32x4 o,
 // kRows rows per wave and loop iteration: 4 for large calls (their loads
 // overlap), 1 for small calls (four times the waves to hide latency with;
 // 8,192 rows: 5.8 us instead of 7.1 us, while 35,840 rows run faster with 4).
+// Large calls write their BF16 rows with non-temporal stores: at 16 MB and
+// more the rows cannot stay in the L2 anyway, and streaming them keeps the
+// caches for the records (35,840 rows: 9.3 us instead of 11.5 us; 1M rows:
+// 0.271 ms instead of 0.286 ms, and the pack that follows in the bulk step
+// 0.391 ms instead of 0.427 ms).
 template <bool kNarrow, int kK, bool kNative, int kRows>
 __global__ __launch_bounds__(256) void unpack_gather_kernel(
     const uint8_t* __restrict__ pool, int64_t pool_rows, const int32_t* __restrict__ physical,
@@ -292,6 +297,8 @@ __global__ __launch_bounds__(256) void unpack_gather_kernel(
       if (row0 + j >= ix.total) continue;
       if (kNative)
         store_native((uint8_t*)out_, row0 + j, o[j], lane);
+      else if (kRows > 1)  // large calls: streaming stores, the rows outsize the caches
+        __builtin_nontemporal_store(o[j], (u32x4*)(out + (row0 + j) * kHeadDim + 8 * lane));
       else
         *(u32x4*)(out + (row0 + j) * kHeadDim + 8 * lane) = o[j];
     }
