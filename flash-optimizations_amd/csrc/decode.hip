@@ -685,8 +685,9 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     } else {
       float* orow = a.ws_o + ((t * a.ws_splits + a.ws_base + split) * a.heads + head0 + h) * kHeadDim +
                     256 * half + col;
+      // streaming stores: the partials are read once, by the combine
 #pragma unroll
-      for (int nt = 0; nt < 16; ++nt) orow[16 * nt] = o[nt][i] * f;
+      for (int nt = 0; nt < 16; ++nt) __builtin_nontemporal_store(o[nt][i] * f, orow + 16 * nt);
     }
   }
 }
