@@ -192,28 +192,28 @@ __device__ __forceinline__ void radix_bits(const uint32_t* key, uint32_t& prefix
   }
 }
 
-// The top seven mantissa bits of the threshold inside its binade [E, E + 1),
-// from a histogram of the binade's keys instead of seven bit-serial counts.
-// Keys hold the exponent from bit kExp up (BF16 keys: the 15-bit magnitude,
-// kExp = 7; FP32 keys: the 31-bit magnitude, kExp = 23). `above` =
-// #{key >= (E + 1) << kExp} < kK <= #{key >= E << kExp}. The wave's 128 LDS
-// bins (zero on entry, zero again on return) count the binade's keys by those
-// seven bits; lane l reads bins 127 - 2l and 126 - 2l, so an inclusive scan
-// over the lanes gives S(m) = #{binade keys with bits >= m}, and the threshold
-// bits are the largest m with above + S(m) >= kK. On return `prefix` holds
-// E and those bits and `at` = #{key >= prefix}, as the bit-serial search
-// leaves them; `tied` = the threshold bin's count (for BF16 keys, the keys
-// equal to the threshold).
-template <int kK, int kExp>
-__device__ __forceinline__ void binade_histogram(const uint32_t* key, uint32_t e, int above,
-                                                 uint32_t* hist, uint32_t& prefix, int& at,
-                                                 int& tied) {
-  const uint32_t base = e << kExp;
+// Seven more bits of the threshold from a histogram instead of seven
+// bit-serial counts. The threshold lies in [base, base + 128 << kShift); keys
+// in that range fall into bin (key - base) >> kShift. `above` = #{key >= base
+// + (128 << kShift)} < kK <= #{key >= base}. Keys are magnitudes: BF16 keys
+// the 15-bit pattern (one level over the binade: base = E << 7, kShift = 0),
+// FP32 keys the 31-bit one (levels with kShift = 16, 9, 2 below base = E << 23,
+// then two bit-serial steps). The wave's 128 LDS bins (zero on entry, zero
+// again on return) count the range's keys; lane l reads bins 127 - 2l and
+// 126 - 2l, so an inclusive scan over the lanes gives S(m) = #{range keys in
+// bins >= m}, and the threshold's bin is the largest m with above + S(m) >=
+// kK. On return `prefix` = base + (m << kShift), `at` = #{key >= prefix}, as
+// the bit-serial search leaves them, and `tied` = the bin's count (for BF16
+// keys, the keys equal to the threshold; otherwise the next level's range).
+template <int kK, int kShift>
+__device__ __forceinline__ void bin_histogram(const uint32_t* key, uint32_t base, int above,
+                                              uint32_t* hist, uint32_t& prefix, int& at,
+                                              int& tied) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t idx = key[i] - base;
-    if (idx < (1u << kExp))
-      __hip_atomic_fetch_add(hist + (idx >> (kExp - 7)), 1u, __ATOMIC_RELAXED,
+    if (idx < (128u << kShift))
+      __hip_atomic_fetch_add(hist + (idx >> kShift), 1u, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_WAVEFRONT);
   }
   wave_lds_sync();
@@ -228,7 +228,7 @@ __device__ __forceinline__ void binade_histogram(const uint32_t* key, uint32_t e
   const int s_lo = __builtin_amdgcn_readlane(incl, l);         // S(126 - 2l)
   const int s_hi = s_lo - __builtin_amdgcn_readlane(lo, l);    // S(127 - 2l)
   const bool upper = s_hi >= need;
-  prefix = base | ((uint32_t)(upper ? 127 - 2 * l : 126 - 2 * l) << (kExp - 7));
+  prefix = base + ((uint32_t)(upper ? 127 - 2 * l : 126 - 2 * l) << kShift);
   at = above + (upper ? s_hi : s_lo);
   tied = upper ? __builtin_amdgcn_readlane(hi, l) : __builtin_amdgcn_readlane(lo, l);
 }
@@ -287,7 +287,8 @@ __device__ __forceinline__ uint32_t keep_at_threshold(const uint32_t* key, const
 // record's threshold exponent `hint` and its neighbours are tried with two or
 // three counts (consecutive records of a layer have thresholds within a
 // binade or two), then mantissa bits 22..16 come from a histogram of that
-// binade (and, for FP32 keys, bits 15..0 bit-serially); when the exponent is
+// binade (FP32 keys: two more histogram levels and two bit-serial steps for
+// bits 15..0); when the exponent is
 // not among them the search runs bit-serially over all key bits. Both
 // ways give the same threshold. `at` is the count at the last accepted step,
 // i.e. #{key >= threshold}; only when it exceeds kK is there a boundary tie to
@@ -326,12 +327,15 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
   }
   if (found) {
     int tied;
-    binade_histogram<kK, kExp>(key, te, above, hist, prefix, at, tied);
     if (kBf16) {
+      bin_histogram<kK, 0>(key, te << 7, above, hist, prefix, at, tied);
       hint = te < 1 ? 1u : (te > 252 ? 252u : te);
       return keep_at_threshold<kK>(key, v, m, prefix, at, tied, ctab);
     }
-    radix_bits<15, 0, kK>(key, prefix, at);
+    bin_histogram<kK, 16>(key, te << 23, above, hist, prefix, at, tied);
+    bin_histogram<kK, 9>(key, prefix, at - tied, hist, prefix, at, tied);
+    bin_histogram<kK, 2>(key, prefix, at - tied, hist, prefix, at, tied);
+    radix_bits<1, 0, kK>(key, prefix, at);
   } else {
     prefix = 0;
     at = 512;
