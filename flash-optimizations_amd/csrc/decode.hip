@@ -923,6 +923,8 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   const int64_t tokens = batch * q_len;
   if (tokens == 0 || heads == 0) return RM_OK;
   if (heads < 0 || heads % 16 || heads > 1024 || bt_stride < max_blocks) return RM_ERR_SHAPE;
+  // an invalid record reads frequency row 0 as a stand-in: a table needs one row
+  if (kPacked && freqs && freq_rows < 1) return RM_ERR_SHAPE;
   if (topk > (int64_t)kPcMaxChunk * c4_max_splits(w) || w.topk > kPcMaxChunk) return RM_ERR_SHAPE;
   if (pool_pages > ((int64_t)1 << 25) || w.pool_pages > ((int64_t)1 << 25))
     return RM_ERR_SHAPE;  // slots fit in int32

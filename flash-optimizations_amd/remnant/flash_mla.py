@@ -98,6 +98,8 @@ def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length
         if freqs_cis.dtype != torch.complex64 or not freqs_cis.is_contiguous():
             raise ValueError("freqs_cis must be a contiguous complex64 tensor")
         freq_ptr, freq_rows = freqs_cis.data_ptr(), freqs_cis.numel() // (config.ROPE_DIM // 2)
+        if freq_rows == 0:
+            raise ValueError("freqs_cis must hold at least one row of 32 frequencies")
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(config.HEAD_DIM)
     if out is None:
@@ -113,10 +115,13 @@ def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length
     bt_stride = block_table.stride(0) if batch > 1 else max(block_table.stride(0),
                                                             block_table.shape[1])
     _, need = get_decode_metadata(batch * q_len, heads, topk, width)
-    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+    if workspace is not None and (workspace.dtype != torch.uint8 or not workspace.is_cuda
+                                  or not workspace.is_contiguous()):
+        raise ValueError("workspace must be a contiguous uint8 tensor on the GPU")
+    if need and (workspace is None or workspace.numel() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     _check_cuda(q, buf, block_table, indices, seqlens, topk_length, sink, freqs_cis, out, lse,
-                sbuf, sidx, slen)
+                sbuf, sidx, slen, workspace)
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     ws_ptr = ptr(workspace) if need else None
     ws_bytes = workspace.numel() * workspace.element_size() if need else 0

@@ -99,8 +99,11 @@ def copy_records(src, src_slots: torch.Tensor, dst, dst_slots: torch.Tensor, *,
         raise ValueError("layer_id out of range")
     _check_cuda(src_slots, dst_slots)
     for pool in (src, dst):
-        if isinstance(pool, HostLatentPool) and not pool.buffer.is_pinned():
-            raise ValueError("host pools used in a transfer must be pinned")
+        # the kernel reads and writes both pools directly: device memory or
+        # pinned host memory only (a pageable buffer would fault the GPU)
+        if not (pool.buffer.is_cuda or pool.buffer.is_pinned()):
+            raise ValueError("pools used in a transfer must live on the GPU or in pinned host "
+                             "memory")
     sbuf = src.buffer if layer_id is None else src.buffer[layer_id]
     dbuf = dst.buffer if layer_id is None else dst.buffer[layer_id]
     fmt = 0 if sfmt == "remnant" else 1

@@ -83,21 +83,25 @@ def native_store_rows(x: torch.Tensor, weight: torch.Tensor, eps: float, loc: to
         raise ValueError("x must be float32 or bfloat16")
     if loc.dtype != torch.int32 or loc.shape != (x.shape[0],) or not loc.is_contiguous():
         raise ValueError("loc must be a contiguous int32 [rows] tensor")
+    if weight.dtype != torch.float32 or weight.shape != (config.HEAD_DIM,) or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous float32 [512] tensor")
     freq_ptr, freq_rows, pos_ptr = None, 0, None
     if freqs_cis is not None:
-        if not freqs_cis.is_complex() or not freqs_cis.is_contiguous():
-            raise ValueError("freqs_cis must be a contiguous complex tensor")
-        if positions is None or positions.dtype != torch.int32 or positions.shape != loc.shape:
-            raise ValueError("positions must be int32 [rows] when freqs_cis is given")
+        if freqs_cis.dtype != torch.complex64 or not freqs_cis.is_contiguous():
+            raise ValueError("freqs_cis must be a contiguous complex64 tensor")
+        if positions is None or positions.dtype != torch.int32 or positions.shape != loc.shape \
+                or not positions.is_contiguous():
+            raise ValueError("positions must be a contiguous int32 [rows] tensor when freqs_cis "
+                             "is given")
         freq_ptr = freqs_cis.data_ptr()
         freq_rows = freqs_cis.numel() // (config.ROPE_DIM // 2)
-        pos_ptr = positions.contiguous().data_ptr()
+        pos_ptr = positions.data_ptr()
     if x.shape[0] == 0:
         return
-    _check_cuda(x, weight, loc, buf, freqs_cis)
+    _check_cuda(x, weight, loc, buf, freqs_cis, positions if freqs_cis is not None else None)
     dtype = 1 if x.dtype == torch.bfloat16 else 0
     _lib.check(_lib.load().rm_native_store_rows(
-        x.data_ptr(), dtype, x.stride(0), weight.contiguous().data_ptr(), float(eps),
+        x.data_ptr(), dtype, x.stride(0), weight.data_ptr(), float(eps),
         loc.data_ptr(), pos_ptr, freq_ptr, freq_rows, x.shape[0], buf.data_ptr(),
         buf.shape[0], _stream()), "rm_native_store_rows")
 

@@ -179,35 +179,89 @@ def test_pack_and_decode_host_validation():
 
 
 def test_cache_format_configuration():
+    ratios = (0, 128, 4, 128, 4, 0, 4)  # C4 layers 2, 4, 6
     try:
         assert remnant.configure_cache_format("direct").packed
-        assert remnant.packed_profile()["record_bytes"] == 328
+        assert remnant.configure_cache_format("direct").record_bytes == 328
         assert not remnant.configure_cache_format("native").packed
-        assert remnant.packed_profile()["record_bytes"] == 584
+        assert config.current().record_bytes == 584
         # the Direct reader is 256-only; 512 and non-multiples of 64 are no profile
         # (docs/agents/numerical-and-validation.md:11-16)
         for bad in (dict(fmt="fp4"), dict(fmt="remnant", keep_count=192),
-                    dict(fmt="remnant", layer_keep_counts=[256, 128]),
+                    dict(fmt="remnant", layer_keep_counts={2: 128}, compression_ratios=ratios),
                     dict(fmt="remnant", decode_impl="triton", keep_count=512),
                     dict(fmt="remnant", decode_impl="triton", keep_count=200),
                     dict(fmt="remnant", decode_impl="triton", keep_count=192.0),
                     dict(fmt="remnant", decode_impl="flashinfer"),
-                    dict(fmt="remnant", decode_impl="triton", layer_keep_counts=[256, 512])):
+                    dict(fmt="remnant", decode_impl="triton", layer_keep_counts={2: 512},
+                         compression_ratios=ratios)):
             with pytest.raises(ValueError):
                 remnant.configure_cache_format(**bad)
         for count in config.KEEP_COUNTS:
             c = remnant.configure_cache_format("remnant", "triton", keep_count=count)
             assert c.decode_impl == "reconstruct" and c.record_bytes == count + 72
-            assert remnant.packed_profile()["page_bytes"] == 64 * (count + 72)
-        c = remnant.configure_cache_format("remnant", "reconstruct",
-                                           layer_keep_counts=[64, 256, 448])
-        assert [c.record_bytes_for(i) for i in range(3)] == [136, 328, 520]
+            assert c.page_bytes == 64 * (count + 72)
+            assert remnant.packed_profile().default_count == count
         import argparse
         p = argparse.ArgumentParser()
         config.add_cli_arguments(p)
         assert config.configure_from_args(p.parse_args(["--kv-cache-format", "direct"])).packed
         with pytest.raises(SystemExit):
             p.parse_args(["--kv-cache-format", "remnant256"])
+    finally:
+        remnant.configure_cache_format("native")
+
+
+def test_profiles_validate_counts_ids_and_atomic_updates():
+    """Per-layer counts name C4 layers of the model (compress_ratios entry 4),
+    in any of the launcher's spellings; a rejected call keeps the previous
+    profile (reference test of the same name, candidate-sglang.patch:939-940;
+    scripts/local/serve.sh:178-185; scripts/local/README.md:993-1013)."""
+    ratios = (0, 128, 4, 128, 4, 0, 4)
+    try:
+        c = remnant.configure_cache_format("remnant", "triton", keep_count=192,
+                                           layer_keep_counts="6:448, 2=64",
+                                           compression_ratios=ratios)
+        prof = remnant.packed_profile()
+        assert isinstance(prof, config.PackedProfile)
+        assert prof == config.PackedProfile(192, ((2, 64), (6, 448)), ratios)
+        assert prof.c4_layers() == (2, 4, 6) and prof.counts() == (64, 192, 448)
+        assert [c.record_bytes_for(i) for i in (2, 4, 6)] == [136, 264, 520]
+        assert [prof.count_for_c4_index(i) for i in range(3)] == [64, 192, 448]
+        assert prof.c4_bytes_per_row() == 136 + 264 + 520  # summed, never padded to 256
+        for spelling in ({2: 64, 6: 448}, [(6, 448), (2, 64)], ["2:64", "6:448"], "2:64 6:448"):
+            again = remnant.configure_cache_format("remnant", "reconstruct", keep_count=192,
+                                                   layer_keep_counts=spelling,
+                                                   compression_ratios=ratios)
+            assert again.profile == prof
+        with pytest.raises(ValueError, match="not a C4 layer"):
+            c.keep_count_for(3)  # a C128 layer has no Packed profile
+        # rejected updates leave the previous profile untouched
+        for bad in (dict(layer_keep_counts={1: 128}),        # C128 layer
+                    dict(layer_keep_counts={0: 128}),        # SWA-only layer
+                    dict(layer_keep_counts={7: 128}),        # beyond the model
+                    dict(layer_keep_counts={2: 512}),        # not a profile
+                    dict(layer_keep_counts=[(2, 64), (2, 128)]),  # two counts for one layer
+                    dict(layer_keep_counts="2-64"),
+                    dict(layer_keep_counts={2: 128}, compression_ratios=None),
+                    dict(layer_keep_counts={-2: 128})):
+            kw = dict(keep_count=192, compression_ratios=ratios)
+            kw.update(bad)
+            with pytest.raises(ValueError):
+                remnant.configure_cache_format("remnant", "triton", **kw)
+            assert remnant.packed_profile() == prof
+        # Direct decode: every C4 layer must keep 256, overrides included
+        with pytest.raises(ValueError, match="256"):
+            remnant.configure_cache_format("remnant", "kernel", layer_keep_counts={4: 128},
+                                           compression_ratios=ratios)
+        assert remnant.packed_profile() == prof
+        d = remnant.configure_cache_format("remnant", "kernel", layer_keep_counts={4: 256},
+                                           compression_ratios=ratios)
+        assert d.profile.counts() == (256, 256, 256)
+        # overrides of non-C4 layers are what the C4-only rule forbids, also for Native
+        with pytest.raises(ValueError):
+            remnant.configure_cache_format("native", layer_keep_counts={3: 128},
+                                           compression_ratios=ratios)
     finally:
         remnant.configure_cache_format("native")
 
@@ -260,6 +314,78 @@ def test_record_transfer_host_validation():
     with pytest.raises(ValueError, match="GPU"):
         host.backup_from_device_all_layer(dev, idx, idx)
     remnant.copy_records(dev, idx[:0], host, idx[:0])  # empty: nothing happens
+
+
+class _FakeCudaTensor:
+    """Stands for a GPU slot list in host-side checks that run before any launch."""
+
+    def __init__(self, t):
+        self._t = t
+        self.dtype, self.shape, self.is_cuda = t.dtype, t.shape, True
+
+    def dim(self):
+        return self._t.dim()
+
+    def is_contiguous(self):
+        return True
+
+
+def test_record_transfer_rejects_pageable_pools():
+    """A pool in pageable host memory (a LatentPool on the CPU, an unpinned
+    host pool) would hand the kernel an address the GPU cannot reach: it is
+    refused before any launch."""
+    idx = _FakeCudaTensor(torch.zeros(4, dtype=torch.int32))
+    dev_cpu = remnant.LatentPool(2, device="cpu")
+    host = remnant.HostLatentPool.like(dev_cpu, pin_memory=False)
+    with pytest.raises(ValueError, match="pinned"):
+        remnant.copy_records(dev_cpu, idx, host, idx)
+    with pytest.raises(ValueError, match="pinned"):
+        remnant.copy_records(host, idx, dev_cpu, idx, layer_id=0)
+
+
+def test_native_store_and_decode_argument_checks():
+    native = remnant.LatentPool(1, fmt="native", device="cpu")
+    x = torch.zeros((2, 512))
+    loc = torch.zeros(2, dtype=torch.int32)
+    pos = torch.zeros(2, dtype=torch.int32)
+    w = torch.ones(512)
+    freqs = torch.ones((8, 32), dtype=torch.complex64)
+    with pytest.raises(ValueError, match="weight"):
+        remnant.native_store_rows(x, w.bfloat16(), 1e-6, loc, pos, freqs, native)
+    with pytest.raises(ValueError, match="weight"):
+        remnant.native_store_rows(x, w[:256], 1e-6, loc, pos, freqs, native)
+    with pytest.raises(ValueError, match="weight"):
+        remnant.native_store_rows(x, torch.ones(1024)[::2], 1e-6, loc, pos, freqs, native)
+    with pytest.raises(ValueError, match="positions"):
+        remnant.native_store_rows(x, w, 1e-6, loc, pos.long(), freqs, native)
+    with pytest.raises(ValueError, match="positions"):
+        remnant.native_store_rows(x, w, 1e-6, loc, torch.zeros(4, dtype=torch.int32)[::2],
+                                  freqs, native)
+    with pytest.raises(ValueError, match="complex64"):
+        remnant.native_store_rows(x, w, 1e-6, loc, pos, freqs.to(torch.complex128), native)
+    with pytest.raises(ValueError, match="GPU"):  # CPU positions with a GPU launch
+        remnant.native_store_rows(x, w, 1e-6, loc, pos, freqs, native)
+    pool = remnant.LatentPool(1, device="cpu")
+    q = torch.zeros((1, 1, 16, 512), dtype=torch.bfloat16)
+    bt = torch.zeros((1, 1), dtype=torch.int32)
+    idx = torch.zeros((1, 1, 64), dtype=torch.int32)
+    with pytest.raises(ValueError, match="at least one row"):
+        remnant.remnant_sparse_decode_fwd(q, pool, bt, idx,
+                                          freqs_cis=torch.ones(16, dtype=torch.complex64))
+    with pytest.raises(ValueError, match="workspace"):
+        remnant.remnant_sparse_decode_fwd(q, pool, bt, idx,
+                                          workspace=torch.zeros(1 << 22, dtype=torch.uint8))
+    with pytest.raises(ValueError, match="workspace"):
+        remnant.remnant_sparse_decode_fwd(q, pool, bt, idx,
+                                          workspace=torch.zeros(1 << 20, dtype=torch.float32))
+    # the C entry point refuses a frequency table without rows
+    lib = _lib.load()
+    _, xq = buf(16384)
+    _, pg = buf(21000)
+    _, s = buf(64)
+    _, f = buf(256)
+    assert lib.rm_remnant_sparse_decode_fwd(xq, 1, 1, 16, pg, 1, s, 4, 4, None, s, 8, None,
+                                            None, f, 0, 0.1, xq, f, None, 0, None) == -2
 
 
 def test_adapter_host_validation():
