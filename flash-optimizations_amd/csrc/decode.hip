@@ -55,15 +55,17 @@ constexpr uint64_t kAddrMask = (1ull << 58) - 1;
 constexpr float kRefSlack = 64.0f;         // log2 headroom above the reference max
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 struct DecodeArgs {
   const uint16_t* q;
-  const uint8_t* pool;
-  int64_t pool_pages;
+  const uint8_t* pool;     // contiguous pages, or the values plane [rows, 256]
+  const uint8_t* bitmaps;  // planes: bitmaps [rows, 8] u64 and scales [rows, 8] u8
+  const uint8_t* scales;
+  int64_t pool_pages;      // pages of 64 records (planes: rows / 64, rounded up)
+  int64_t pool_rows;
   const int32_t* block_table;
   int64_t bt_stride;
   int64_t max_blocks;
@@ -90,8 +92,7 @@ struct DecodeArgs {
 // Two E4M3 codes (bytes 0-1, or 2-3 with kHi) times scale -> two BF16 (exact).
 template <bool kHi>
 __device__ __forceinline__ uint32_t cvt2(uint32_t codes, float scale) {
-  bf16x2 r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(codes, scale, kHi);
-  return __builtin_bit_cast(uint32_t, r);
+  return fp8_pair_to_bf16<kHi>(codes, scale);
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -209,9 +210,10 @@ __device__ __forceinline__ float max_over_rows(float x) {
 // One workgroup's share: split `split` of list `a` (a C4 top-k list through
 // the block table, or with a.block_table == nullptr a list of pool slots), for
 // kHG groups of 16 heads: every expanded record serves all of them.
-template <bool kPacked, int kHG>
+template <bool kPacked, int kHG, bool kPlanes = false>
 __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>* sm,
                                           const int split) {
+  static_assert(kPacked || !kPlanes, "planes hold Packed records");
   using G = PcGeo<kPacked>;
   constexpr int kPcConsumers = PcRoles<kHG>::kConsumers;
   constexpr int kPcThreads = PcRoles<kHG>::kThreads;
@@ -282,11 +284,15 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
         ok = r >= 0;
         page = r >> 6;
       }
-      ok = ok && page >= 0 && page < a.pool_pages;
+      ok = ok && page >= 0 && page < a.pool_pages && page * 64 + (r & 63) < a.pool_rows;
       if (kPacked && a.freqs) ok = ok && r * 4 < a.freq_rows;
     }
-    const uint8_t* pg = a.pool + (ok ? page : 0) * G::kPage;
-    row_tab[i] = ok ? (uint64_t)(pg + (r & 63) * G::kData) | (kPacked ? 0 : (uint64_t)(r & 63) << 58)
+    // planes: the record's values row (16-byte aligned); its bitmap and scale
+    // rows sit at a quarter and a 32nd of the values offset in their planes
+    const uint8_t* pg = kPlanes ? a.pool + (ok ? page : 0) * 64 * kCodeBytes
+                                : a.pool + (ok ? page : 0) * G::kPage;
+    row_tab[i] = ok ? (uint64_t)(pg + (r & 63) * (kPlanes ? kCodeBytes : G::kData)) |
+                          (kPacked ? 0 : (uint64_t)(r & 63) << 58)
                     : stand_in;
     if (kPacked) aux_tab[i] = a.freqs ? (uint64_t)(a.freqs + (ok ? r : 0) * 4 * 64) : (uint64_t)a.q;
   }
@@ -338,7 +344,14 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
         uint64_t src;
         if (c < G::kRecPieces) {
           const int piece = c - (c / G::kPieces) * G::kPieces;
-          src = (rw[j] & (kPacked ? ~(uint64_t)15 : kAddrMask & ~(uint64_t)15)) + 16 * piece;
+          if (kPlanes && !(rw[j] & 1u)) {  // codes 0..15, bitmap 16..19, scales 20
+            const uint64_t off = rw[j] - (uint64_t)a.pool;  // slot * 256
+            src = piece < 16 ? rw[j] + 16 * piece
+                  : piece < 20 ? (uint64_t)a.bitmaps + (off >> 2) + 16 * (piece - 16)
+                               : (uint64_t)a.scales + ((off >> 5) & ~(uint64_t)15);
+          } else {
+            src = (rw[j] & (kPacked ? ~(uint64_t)15 : kAddrMask & ~(uint64_t)15)) + 16 * piece;
+          }
         } else {  // Packed RoPE piece (c - kRecPieces) / 8, or a filler lane
           src = rw[j] + 16 * ((c - G::kRecPieces) >> 3);
         }
@@ -381,10 +394,13 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     auto gather = [&](auto bufc, const Head& h, Gath& gt) {
       constexpr int B = decltype(bufc)::value;
       const uint8_t* st = &raw[p][B][0] + pi * G::kPitch;
-      const bool valid = !(h.row & 1u), odd = (h.row & 8u) != 0;
+      // odd: codes and bitmap staged 8 bytes in (a contiguous record from an
+      // odd pool row); sodd: the scales 8 bytes in (planes: an odd slot)
+      const bool valid = !(h.row & 1u), odd = !kPlanes && (h.row & 8u) != 0;
+      const bool sodd = kPlanes ? (((h.row - (uint64_t)a.pool) >> 8) & 1u) != 0 : odd;
       const uint32_t wlo = valid ? (odd ? h.w[2] : h.w[0]) : 0u;
       const uint32_t whi = valid ? (odd ? h.w[3] : h.w[1]) : 0u;
-      const uint32_t sw = valid ? (odd ? h.sc1 : h.sc0) : 0u;
+      const uint32_t sw = valid ? (sodd ? h.sc1 : h.sc0) : 0u;
       gt.scale = exp2i((int)((sw >> (8 * (pw & 3))) & 0xffu) - 127);
       // codes before this word: exclusive prefix over the record's lanes
       // i + 8 w. A 16-lane row holds words 2k, 2k + 1: pair sums in the row
@@ -692,10 +708,10 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
   }
 }
 
-template <int kHG>
+template <int kHG, bool kPlanes>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void packed_decode_pc_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[sizeof(PcShared<true>)];
-  decode_pc<true, kHG>(a, reinterpret_cast<PcShared<true>*>(smem), blockIdx.x);
+  decode_pc<true, kHG, kPlanes>(a, reinterpret_cast<PcShared<true>*>(smem), blockIdx.x);
 }
 template <int kHG>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_decode_pc_kernel(DecodeArgs a) {
@@ -704,18 +720,18 @@ __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_decode_pc_kerne
 }
 // C4 list and window rows in one launch: workgroups x < c4.splits take a C4
 // split, the last column the window rows (Native records).
-template <bool kPacked, int kHG>
+template <bool kPacked, int kHG, bool kPlanes = false>
 __device__ __forceinline__ void decode_joint(const DecodeArgs& c4, const DecodeArgs& swa) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kPcSmemBytes];
   if ((int)blockIdx.x < c4.splits)
-    decode_pc<kPacked, kHG>(c4, reinterpret_cast<PcShared<kPacked>*>(smem), blockIdx.x);
+    decode_pc<kPacked, kHG, kPlanes>(c4, reinterpret_cast<PcShared<kPacked>*>(smem), blockIdx.x);
   else
     decode_pc<false, kHG>(swa, reinterpret_cast<PcShared<false>*>(smem), 0);
 }
-template <int kHG>
+template <int kHG, bool kPlanes>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void packed_swa_decode_pc_kernel(
     DecodeArgs c4, DecodeArgs swa) {
-  decode_joint<true, kHG>(c4, swa);
+  decode_joint<true, kHG, kPlanes>(c4, swa);
 }
 template <int kHG>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_swa_decode_pc_kernel(
@@ -909,17 +925,39 @@ size_t ws_bytes(int64_t tokens, int64_t heads, int64_t slots) {
   return slots > 1 ? (size_t)(tokens * slots * heads) * (kHeadDim + 1) * sizeof(float) : 0;
 }
 
+// Where the C4 records live: contiguous pages (bitmaps == nullptr) or the
+// three planes of `rows` Packed records.
+struct Src {
+  const uint8_t* pool = nullptr;
+  const uint8_t* bitmaps = nullptr;
+  const uint8_t* scales = nullptr;
+  int64_t pages = 0;
+  int64_t rows = 0;
+  bool planes() const { return bitmaps != nullptr; }
+};
+Src paged(const uint8_t* pool, int64_t pages) {
+  Src r;
+  r.pool = pool;
+  r.pages = pages;
+  r.rows = pages * kPageRecords;
+  return r;
+}
+
 template <bool kPacked>
 int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads,
-                  const uint8_t* pool, int64_t pool_pages, const int32_t* block_table,
+                  const Src& src, const int32_t* block_table,
                   int64_t bt_stride, int64_t max_blocks, const int32_t* seqlens,
                   const int32_t* indices, int64_t topk, const int32_t* topk_length,
                   const Swa& w, const float* sink, const float* freqs, int64_t freq_rows,
                   float scale, uint16_t* out, float* lse, void* workspace,
                   size_t workspace_bytes, void* stream) {
+  const uint8_t* pool = src.pool;
+  const int64_t pool_pages = src.pages;
   if (batch < 0 || q_len < 0 || topk < 0 || pool_pages < 0 || max_blocks < 0 || freq_rows < 0 ||
-      w.topk < 0 || w.pool_pages < 0)
+      w.topk < 0 || w.pool_pages < 0 || src.rows < 0)
     return RM_ERR_SHAPE;
+  // planes: the scale rows of slots 2k and 2k + 1 are copied as one 16-byte piece
+  if (src.planes() && (src.rows & 1)) return RM_ERR_SHAPE;
   const int64_t tokens = batch * q_len;
   if (tokens == 0 || heads == 0) return RM_OK;
   if (heads < 0 || heads % 16 || heads > 1024 || bt_stride < max_blocks) return RM_ERR_SHAPE;
@@ -931,8 +969,10 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   if (!q || !out || !lse || (topk > 0 && (!indices || !pool || !block_table)) ||
       (w.topk > 0 && (!w.indices || !w.pool)))
     return RM_ERR_NULL;
+  if (topk > 0 && src.planes() && !src.scales) return RM_ERR_NULL;
   if (!aligned(q, 16) || !aligned(out, 16) || (pool && !aligned(pool, 16)) ||
-      (w.pool && !aligned(w.pool, 16)) || (freqs && !aligned(freqs, 16)))
+      (w.pool && !aligned(w.pool, 16)) || (freqs && !aligned(freqs, 16)) ||
+      (src.planes() && !(aligned(src.bitmaps, 16) && aligned(src.scales, 16))))
     return RM_ERR_ALIGN;
   if (tokens > 65535) return RM_ERR_SHAPE;
   const Plan plan = plan_pc(tokens, heads, topk, c4_max_splits(w), w.topk > 0);
@@ -943,7 +983,10 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   DecodeArgs a;
   a.q = q;
   a.pool = pool;
+  a.bitmaps = src.bitmaps;
+  a.scales = src.scales;
   a.pool_pages = pool_pages;
+  a.pool_rows = src.rows;
   a.block_table = block_table;
   a.bt_stride = bt_stride;
   a.max_blocks = max_blocks;
@@ -973,7 +1016,10 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
     // the window rows are one more split, read by the Native path of the same launch
     DecodeArgs b = a;
     b.pool = w.pool;
+    b.bitmaps = nullptr;
+    b.scales = nullptr;
     b.pool_pages = w.pool_pages;
+    b.pool_rows = w.pool_pages * kPageRecords;
     b.block_table = nullptr;  // entries are pool slots
     b.seqlens = nullptr;
     b.indices = w.indices;
@@ -985,20 +1031,24 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
     b.splits = 1;
     b.ws_base = plan.splits;
     const dim3 grid((unsigned)slots, (unsigned)tokens, zblocks);
-    if (hg == 2)
-      hipLaunchKernelGGL(kPacked ? packed_swa_decode_pc_kernel<2> : native_swa_decode_pc_kernel<2>,
-                         grid, block, 0, s, a, b);
+    void (*kern)(DecodeArgs, DecodeArgs);
+    if (!kPacked)
+      kern = hg == 2 ? native_swa_decode_pc_kernel<2> : native_swa_decode_pc_kernel<1>;
+    else if (src.planes())
+      kern = hg == 2 ? packed_swa_decode_pc_kernel<2, true> : packed_swa_decode_pc_kernel<1, true>;
     else
-      hipLaunchKernelGGL(kPacked ? packed_swa_decode_pc_kernel<1> : native_swa_decode_pc_kernel<1>,
-                         grid, block, 0, s, a, b);
+      kern = hg == 2 ? packed_swa_decode_pc_kernel<2, false> : packed_swa_decode_pc_kernel<1, false>;
+    hipLaunchKernelGGL(kern, grid, block, 0, s, a, b);
   } else {
     const dim3 grid((unsigned)plan.splits, (unsigned)tokens, zblocks);
-    if (hg == 2)
-      hipLaunchKernelGGL(kPacked ? packed_decode_pc_kernel<2> : native_decode_pc_kernel<2>, grid,
-                         block, 0, s, a);
+    void (*kern)(DecodeArgs);
+    if (!kPacked)
+      kern = hg == 2 ? native_decode_pc_kernel<2> : native_decode_pc_kernel<1>;
+    else if (src.planes())
+      kern = hg == 2 ? packed_decode_pc_kernel<2, true> : packed_decode_pc_kernel<1, true>;
     else
-      hipLaunchKernelGGL(kPacked ? packed_decode_pc_kernel<1> : native_decode_pc_kernel<1>, grid,
-                         block, 0, s, a);
+      kern = hg == 2 ? packed_decode_pc_kernel<2, false> : packed_decode_pc_kernel<1, false>;
+    hipLaunchKernelGGL(kern, grid, block, 0, s, a);
   }
   if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   if (slots > 1) {
@@ -1043,7 +1093,7 @@ extern "C" int rm_remnant_sparse_decode_fwd(
     const int32_t* topk_length, const float* sink, const float* freqs, int64_t freq_rows,
     float softmax_scale, uint16_t* out, float* lse, void* workspace, size_t workspace_bytes,
     void* stream) {
-  return launch_decode<true>(q, batch, q_len, heads, pool, pool_pages, block_table,
+  return launch_decode<true>(q, batch, q_len, heads, paged(pool, pool_pages), block_table,
                              block_table_stride, max_blocks, seqlens, indices, topk, topk_length,
                              Swa(), sink, freqs, freq_rows, softmax_scale, out, lse, workspace,
                              workspace_bytes, stream);
@@ -1063,10 +1113,40 @@ extern "C" int rm_remnant_sparse_decode_swa_fwd(
   w.indices = swa_indices;
   w.topk = swa_topk;
   w.length = swa_length;
-  return launch_decode<true>(q, batch, q_len, heads, pool, pool_pages, block_table,
+  return launch_decode<true>(q, batch, q_len, heads, paged(pool, pool_pages), block_table,
                              block_table_stride, max_blocks, seqlens, indices, topk, topk_length,
                              w, sink, freqs, freq_rows, softmax_scale, out, lse, workspace,
                              workspace_bytes, stream);
+}
+
+extern "C" int rm_remnant_sparse_decode_planes_fwd(
+    const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads, const uint8_t* values,
+    const uint64_t* bitmaps, const uint8_t* scales, int64_t pool_rows,
+    const int32_t* block_table, int64_t block_table_stride, int64_t max_blocks,
+    const int32_t* seqlens, const int32_t* indices, int64_t topk, const int32_t* topk_length,
+    const uint8_t* swa_pool, int64_t swa_pool_pages, const int32_t* swa_indices,
+    int64_t swa_topk, const int32_t* swa_length, const float* sink, const float* freqs,
+    int64_t freq_rows, float softmax_scale, uint16_t* out, float* lse, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  if (pool_rows < 0 || pool_rows > ((int64_t)1 << 31)) return RM_ERR_SHAPE;
+  if (!bitmaps && topk > 0) return RM_ERR_NULL;
+  Src src;
+  src.pool = values;
+  src.bitmaps = (const uint8_t*)bitmaps;
+  src.scales = scales;
+  src.rows = pool_rows;
+  src.pages = (pool_rows + kPageRecords - 1) / kPageRecords;
+  if (!bitmaps) src = paged(values, 0);  // nothing is read
+  Swa w;
+  w.pool = swa_pool;
+  w.pool_pages = swa_pool_pages;
+  w.indices = swa_indices;
+  w.topk = swa_topk;
+  w.length = swa_length;
+  return launch_decode<true>(q, batch, q_len, heads, src, block_table, block_table_stride,
+                             max_blocks, seqlens, indices, topk, topk_length, w, sink, freqs,
+                             freq_rows, softmax_scale, out, lse, workspace, workspace_bytes,
+                             stream);
 }
 
 extern "C" int rm_native_sparse_decode_fwd(
@@ -1075,7 +1155,7 @@ extern "C" int rm_native_sparse_decode_fwd(
     int64_t max_blocks, const int32_t* seqlens, const int32_t* indices, int64_t topk,
     const int32_t* topk_length, const float* sink, float softmax_scale, uint16_t* out,
     float* lse, void* workspace, size_t workspace_bytes, void* stream) {
-  return launch_decode<false>(q, batch, q_len, heads, pool, pool_pages, block_table,
+  return launch_decode<false>(q, batch, q_len, heads, paged(pool, pool_pages), block_table,
                               block_table_stride, max_blocks, seqlens, indices, topk,
                               topk_length, Swa(), sink, nullptr, 0, softmax_scale, out, lse,
                               workspace, workspace_bytes, stream);
@@ -1095,7 +1175,7 @@ extern "C" int rm_native_sparse_decode_swa_fwd(
   w.indices = swa_indices;
   w.topk = swa_topk;
   w.length = swa_length;
-  return launch_decode<false>(q, batch, q_len, heads, pool, pool_pages, block_table,
+  return launch_decode<false>(q, batch, q_len, heads, paged(pool, pool_pages), block_table,
                               block_table_stride, max_blocks, seqlens, indices, topk,
                               topk_length, w, sink, nullptr, 0, softmax_scale, out, lse,
                               workspace, workspace_bytes, stream);

@@ -30,17 +30,6 @@ constexpr int kWaves = 4;
 constexpr int kRowsBulk = 4;   // rows per wave and loop iteration for large calls
 constexpr int kSmallCall = 16384;  // below this many rows, one row per wave
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// Two E4M3 codes (bytes 0-1, or 2-3 with kHi) times scale -> two BF16. The
-// hardware conversion equals BF16-rounding the FP32 product code * scale for
-// every finite code and every finite UE8M0 scale.
-template <bool kHi>
-__device__ __forceinline__ uint32_t cvt2(uint32_t codes, float scale) {
-  bf16x2 r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(codes, scale, kHi);
-  return __builtin_bit_cast(uint32_t, r);
-}
-
 // Byte-addressed read of another lane's register (ds_bpermute).
 __device__ __forceinline__ uint32_t from_lane(uint32_t v, int src_lane) {
   return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane << 2, (int)v);
@@ -100,8 +89,8 @@ __device__ __forceinline__ u32x4 dequant_lane(u32x2 piece, u32x2 extra, int lane
                                          : __builtin_amdgcn_readlane(extra[1], 0);
   const uint32_t sc = word < 4 ? sc_lo : sc_hi;
   const float scale = exp2i((int)((sc >> (8 * (word & 3))) & 0xffu) - 127);
-  return u32x4{cvt2<false>(c03, scale), cvt2<true>(c03, scale), cvt2<false>(c47, scale),
-               cvt2<true>(c47, scale)};
+  return u32x4{fp8_pair_to_bf16<false>(c03, scale), fp8_pair_to_bf16<true>(c03, scale),
+               fp8_pair_to_bf16<false>(c47, scale), fp8_pair_to_bf16<true>(c47, scale)};
 }
 
 // Row indexing. The narrow form (every index and element offset below 2^31)
@@ -129,8 +118,6 @@ __device__ __forceinline__ void split_row(int64_t row, const Index& ix, int64_t&
     k = row - q * ix.nk;
   }
 }
-
-typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 // Native 584-byte record of the lane-distributed BF16 row `o` (lane l holds
 // coordinates 8l..8l+7) at workspace row `row` of a Native page layout: the
@@ -162,10 +149,10 @@ __device__ __forceinline__ void store_native(uint8_t* out, int64_t row, u32x4 o,
       p[i] = bf16x2{__builtin_bit_cast(__bf16, (uint16_t)(o[i] & 0xffffu)),
                     __builtin_bit_cast(__bf16, (uint16_t)(o[i] >> 16))};
     s16x2 c01 = {0, 0}, c45 = {0, 0};
-    c01 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c01, p[0], scale, false);
-    c01 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c01, p[1], scale, true);
-    c45 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c45, p[2], scale, false);
-    c45 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c45, p[3], scale, true);
+    c01 = fp8_pair<false>(c01, p[0], scale);
+    c01 = fp8_pair<true>(c01, p[1], scale);
+    c45 = fp8_pair<false>(c45, p[2], scale);
+    c45 = fp8_pair<true>(c45, p[3], scale);
     *(u32x2*)(data + 8 * lane) = u32x2{__builtin_bit_cast(uint32_t, c01), __builtin_bit_cast(uint32_t, c45)};
   } else {
     *(u32x4*)(data + kNopeDim + 16 * (lane - kNopeDim / 8)) = o;
@@ -189,9 +176,9 @@ __device__ __forceinline__ void store_native(uint8_t* out, int64_t row, u32x4 o,
 // caches for the records (35,840 rows: 9.3 us instead of 11.5 us; 1M rows:
 // 0.271 ms instead of 0.286 ms, and the pack that follows in the bulk step
 // 0.391 ms instead of 0.427 ms).
-template <bool kNarrow, int kK, bool kNative, int kRows>
+template <bool kNarrow, int kK, bool kNative, int kRows, bool kPlanes>
 __global__ __launch_bounds__(256) void unpack_gather_kernel(
-    const uint8_t* __restrict__ pool, int64_t pool_rows, const int32_t* __restrict__ physical,
+    PackedSrc src, int64_t pool_rows, const int32_t* __restrict__ physical,
     const int32_t* __restrict__ raw, const int32_t* __restrict__ lengths, Index ix,
     const float* __restrict__ freqs, int64_t freq_rows, void* __restrict__ out_) {
   uint16_t* const out = (uint16_t*)out_;
@@ -220,7 +207,8 @@ __global__ __launch_bounds__(256) void unpack_gather_kernel(
   // loads are issued together, so their latencies overlap
   for (int64_t row0 = ((int64_t)blockIdx.x * kWaves + wave) * kRows; row0 < ix.total;
        row0 += (int64_t)gridDim.x * kWaves * kRows) {
-    const uint8_t* rec[kRows];
+    const uint8_t* rec[kRows];   // this lane's 8-byte piece of the record
+    const uint8_t* srec[kRows];  // bytes 512..519 (448 survivors: the scales)
     int64_t rr[kRows];
     bool valid[kRows];
 #pragma unroll
@@ -241,7 +229,17 @@ __global__ __launch_bounds__(256) void unpack_gather_kernel(
       bool v = row < ix.total && k < len && p >= 0 && p < pool_rows;
       if (freqs) v = v && r >= 0 && r * 4 < freq_rows;
       const uint32_t pp = v ? (uint32_t)p : 0u;  // pool rows fit in int32
-      rec[j] = pool + (uint64_t)(pp >> 6) * (kPageRecords * kBytes) + (pp & 63u) * kBytes;
+      // contiguous pages hold 64 records each back to back: slot pp starts
+      // pp * kBytes into the pool; planes: this lane's piece of each plane
+      if (kPlanes) {
+        rec[j] = lane < kK / 8 ? src.values + (uint64_t)pp * kK + 8 * lane
+                 : lane < kK / 8 + 8 ? src.bitmaps + (uint64_t)pp * kBitmapBytes + 8 * (lane - kK / 8)
+                                     : src.scales + (uint64_t)pp * kScaleBytes;
+        srec[j] = src.scales + (uint64_t)pp * kScaleBytes;
+      } else {
+        rec[j] = src.values + (uint64_t)pp * kBytes + 8 * lane;
+        srec[j] = src.values + (uint64_t)pp * kBytes + 512;
+      }
       rr[j] = r;
       valid[j] = v;
     }
@@ -252,8 +250,8 @@ __global__ __launch_bounds__(256) void unpack_gather_kernel(
     for (int j = 0; j < kRows; ++j) {
       piece[j] = u32x2{0u, 0u};
       extra[j] = u32x2{0u, 0u};
-      if (valid[j] && lane < kPieces) piece[j] = *(const u32x2*)(rec[j] + 8 * lane);
-      if (kBytes > 512 && valid[j]) extra[j] = *(const u32x2*)(rec[j] + 512);
+      if (valid[j] && lane < kPieces) piece[j] = *(const u32x2*)rec[j];
+      if (kBytes > 512 && valid[j]) extra[j] = *(const u32x2*)srec[j];
     }
     f32x4 fa[kRows], fb[kRows];
     const bool tail = freqs && lane >= kNopeDim / 8;
@@ -308,7 +306,8 @@ __global__ __launch_bounds__(256) void unpack_gather_kernel(
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 struct Launch {
-  const uint8_t* pool;
+  PackedSrc src;
+  bool planes;
   int64_t pool_rows;
   const int32_t *physical, *raw, *lengths;
   Index ix;
@@ -317,18 +316,26 @@ struct Launch {
   void* out;
 };
 
-template <int kK, bool kNative, int kRows>
-void launch_rows(bool narrow, const Launch& a, hipStream_t s) {
+template <int kK, bool kNative, int kRows, bool kPlanes>
+void launch_rows_layout(bool narrow, const Launch& a, hipStream_t s) {
   int64_t blocks = (a.ix.total + kWaves * kRows - 1) / (kWaves * kRows);
   if (blocks > 256 * 64) blocks = 256 * 64;
   if (narrow)
-    hipLaunchKernelGGL((unpack_gather_kernel<true, kK, kNative, kRows>), dim3((unsigned)blocks),
-                       dim3(256), 0, s, a.pool, a.pool_rows, a.physical, a.raw, a.lengths, a.ix,
-                       a.freqs, a.freq_rows, a.out);
+    hipLaunchKernelGGL((unpack_gather_kernel<true, kK, kNative, kRows, kPlanes>),
+                       dim3((unsigned)blocks), dim3(256), 0, s, a.src, a.pool_rows, a.physical,
+                       a.raw, a.lengths, a.ix, a.freqs, a.freq_rows, a.out);
   else
-    hipLaunchKernelGGL((unpack_gather_kernel<false, kK, kNative, kRows>), dim3((unsigned)blocks),
-                       dim3(256), 0, s, a.pool, a.pool_rows, a.physical, a.raw, a.lengths, a.ix,
-                       a.freqs, a.freq_rows, a.out);
+    hipLaunchKernelGGL((unpack_gather_kernel<false, kK, kNative, kRows, kPlanes>),
+                       dim3((unsigned)blocks), dim3(256), 0, s, a.src, a.pool_rows, a.physical,
+                       a.raw, a.lengths, a.ix, a.freqs, a.freq_rows, a.out);
+}
+
+template <int kK, bool kNative, int kRows>
+void launch_rows(bool narrow, const Launch& a, hipStream_t s) {
+  if (a.planes)
+    launch_rows_layout<kK, kNative, kRows, true>(narrow, a, s);
+  else
+    launch_rows_layout<kK, kNative, kRows, false>(narrow, a, s);
 }
 
 template <int kK, bool kNative = false>
@@ -341,18 +348,24 @@ void launch_unpack(bool narrow, const Launch& a, hipStream_t s) {
 
 // Argument checks and launch geometry shared by the reader entry points.
 // Returns RM_OK with a.out == nullptr when there is nothing to launch.
-int prepare(const uint8_t* pool, int64_t pool_pages, const int32_t* physical, int64_t ps_q,
+// Contiguous pools are 16-byte aligned; each plane of a plane-layout pool is
+// 8-byte aligned (its rows are multiples of 8 bytes).
+int prepare(PackedSrc src, bool planes, int64_t pool_rows, const int32_t* physical, int64_t ps_q,
             int64_t ps_k, const int32_t* raw, int64_t rs_q, int64_t rs_k, const int32_t* lengths,
             int64_t ls, int64_t n_queries, int64_t selected_k, const float* freqs,
             int64_t freq_rows, void* out, Launch& a, bool& narrow) {
   a.out = nullptr;
-  if (n_queries < 0 || selected_k < 0 || pool_pages < 0 || freq_rows < 0) return RM_ERR_SHAPE;
+  if (n_queries < 0 || selected_k < 0 || pool_rows < 0 || freq_rows < 0) return RM_ERR_SHAPE;
   const int64_t total = n_queries * selected_k;
   if (total == 0) return RM_OK;
-  if (!pool || !physical || !lengths || !out || (freqs && !raw)) return RM_ERR_NULL;
-  if (!aligned(pool, 16) || !aligned(out, 16) || (freqs && !aligned(freqs, 16)))
+  if (!src.values || (planes && (!src.bitmaps || !src.scales)) || !physical || !lengths ||
+      !out || (freqs && !raw))
+    return RM_ERR_NULL;
+  if (!aligned(out, 16) || (freqs && !aligned(freqs, 16))) return RM_ERR_ALIGN;
+  if (planes ? !(aligned(src.values, 8) && aligned(src.bitmaps, 8) && aligned(src.scales, 8))
+             : !aligned(src.values, 16))
     return RM_ERR_ALIGN;
-  if (pool_pages > ((int64_t)1 << 25)) return RM_ERR_SHAPE;  // pool rows fit in int32
+  if (pool_rows > ((int64_t)1 << 31)) return RM_ERR_SHAPE;  // pool rows fit in int32
   Index ix;
   ix.ps_q = ps_q;
   ix.ps_k = ps_k;
@@ -378,26 +391,20 @@ int prepare(const uint8_t* pool, int64_t pool_pages, const int32_t* physical, in
     ix.magic = (uint32_t)(((((uint64_t)1 << l) - d) << 32) / d + 1);
     ix.shift = (uint32_t)(l - 1);
   }
-  a = Launch{pool, pool_pages * kPageRecords, physical, raw, lengths, ix, freqs, freq_rows, out};
+  a = Launch{src, planes, pool_rows, physical, raw, lengths, ix, freqs, freq_rows, out};
   return RM_OK;
 }
 
-}  // namespace
-
-extern "C" int rm_unpack_gather_bf16_k(const uint8_t* pool, int64_t pool_pages, int keep_count,
-                                       const int32_t* physical, int64_t physical_stride_q,
-                                       int64_t physical_stride_k, const int32_t* raw,
-                                       int64_t raw_stride_q, int64_t raw_stride_k,
-                                       const int32_t* lengths, int64_t length_stride,
-                                       int64_t n_queries, int64_t selected_k,
-                                       const float* freqs, int64_t freq_rows, uint16_t* out,
-                                       void* stream) {
+int launch_reader(PackedSrc src, bool planes, int64_t pool_rows, int keep_count,
+                  const int32_t* physical, int64_t ps_q, int64_t ps_k, const int32_t* raw,
+                  int64_t rs_q, int64_t rs_k, const int32_t* lengths, int64_t ls,
+                  int64_t n_queries, int64_t selected_k, const float* freqs, int64_t freq_rows,
+                  uint16_t* out, void* stream) {
   if (keep_count < 64 || keep_count > 448 || keep_count % 64) return RM_ERR_SHAPE;
   Launch a;
   bool narrow = false;
-  const int st = prepare(pool, pool_pages, physical, physical_stride_q, physical_stride_k, raw,
-                         raw_stride_q, raw_stride_k, lengths, length_stride, n_queries,
-                         selected_k, freqs, freq_rows, out, a, narrow);
+  const int st = prepare(src, planes, pool_rows, physical, ps_q, ps_k, raw, rs_q, rs_k, lengths,
+                         ls, n_queries, selected_k, freqs, freq_rows, out, a, narrow);
   if (st != RM_OK || !a.out) return st;
   hipStream_t s = (hipStream_t)stream;
   switch (keep_count) {
@@ -412,6 +419,64 @@ extern "C" int rm_unpack_gather_bf16_k(const uint8_t* pool, int64_t pool_pages, 
   return hipGetLastError() == hipSuccess ? RM_OK : RM_ERR_LAUNCH;
 }
 
+int launch_adapter(PackedSrc src, bool planes, int64_t pool_rows, const int32_t* physical,
+                   int64_t ps_q, int64_t ps_k, const int32_t* raw, int64_t rs_q, int64_t rs_k,
+                   const int32_t* lengths, int64_t ls, int64_t n_queries, int64_t selected_k,
+                   const float* freqs, int64_t freq_rows, uint8_t* native, int64_t native_pages,
+                   void* stream) {
+  if (native_pages < 0 || n_queries < 0 || selected_k < 0) return RM_ERR_SHAPE;
+  if (n_queries * selected_k > native_pages * kPageRecords) return RM_ERR_SHAPE;
+  Launch a;
+  bool narrow = false;
+  const int st = prepare(src, planes, pool_rows, physical, ps_q, ps_k, raw, rs_q, rs_k, lengths,
+                         ls, n_queries, selected_k, freqs, freq_rows, native, a, narrow);
+  if (st != RM_OK || !a.out) return st;
+  launch_unpack<kKeep, true>(narrow, a, (hipStream_t)stream);
+  return hipGetLastError() == hipSuccess ? RM_OK : RM_ERR_LAUNCH;
+}
+
+PackedSrc contiguous(const uint8_t* pool) { return PackedSrc{pool, nullptr, nullptr}; }
+PackedSrc plane_src(const uint8_t* values, const uint64_t* bitmaps, const uint8_t* scales) {
+  return PackedSrc{values, (const uint8_t*)bitmaps, scales};
+}
+// Pool pages -> rows. A page count past the int32 slot range (or negative)
+// maps to a row count that prepare() rejects.
+int64_t page_rows(int64_t pool_pages) {
+  if (pool_pages < 0) return -1;
+  return pool_pages > ((int64_t)1 << 25) ? ((int64_t)1 << 32) : pool_pages * kPageRecords;
+}
+
+}  // namespace
+
+extern "C" int rm_unpack_gather_bf16_k(const uint8_t* pool, int64_t pool_pages, int keep_count,
+                                       const int32_t* physical, int64_t physical_stride_q,
+                                       int64_t physical_stride_k, const int32_t* raw,
+                                       int64_t raw_stride_q, int64_t raw_stride_k,
+                                       const int32_t* lengths, int64_t length_stride,
+                                       int64_t n_queries, int64_t selected_k,
+                                       const float* freqs, int64_t freq_rows, uint16_t* out,
+                                       void* stream) {
+  return launch_reader(contiguous(pool), false, page_rows(pool_pages), keep_count, physical,
+                       physical_stride_q, physical_stride_k, raw, raw_stride_q, raw_stride_k,
+                       lengths, length_stride, n_queries, selected_k, freqs, freq_rows, out,
+                       stream);
+}
+
+extern "C" int rm_unpack_gather_bf16_planes(const uint8_t* values, const uint64_t* bitmaps,
+                                            const uint8_t* scales, int64_t rows, int keep_count,
+                                            const int32_t* physical, int64_t physical_stride_q,
+                                            int64_t physical_stride_k, const int32_t* raw,
+                                            int64_t raw_stride_q, int64_t raw_stride_k,
+                                            const int32_t* lengths, int64_t length_stride,
+                                            int64_t n_queries, int64_t selected_k,
+                                            const float* freqs, int64_t freq_rows, uint16_t* out,
+                                            void* stream) {
+  return launch_reader(plane_src(values, bitmaps, scales), true, rows, keep_count, physical,
+                       physical_stride_q, physical_stride_k, raw, raw_stride_q, raw_stride_k,
+                       lengths, length_stride, n_queries, selected_k, freqs, freq_rows, out,
+                       stream);
+}
+
 extern "C" int rm_packed_to_native(const uint8_t* pool, int64_t pool_pages,
                                    const int32_t* physical, int64_t physical_stride_q,
                                    int64_t physical_stride_k, const int32_t* raw,
@@ -420,16 +485,25 @@ extern "C" int rm_packed_to_native(const uint8_t* pool, int64_t pool_pages,
                                    int64_t n_queries, int64_t selected_k, const float* freqs,
                                    int64_t freq_rows, uint8_t* native, int64_t native_pages,
                                    void* stream) {
-  if (native_pages < 0 || n_queries < 0 || selected_k < 0) return RM_ERR_SHAPE;
-  if (n_queries * selected_k > native_pages * kPageRecords) return RM_ERR_SHAPE;
-  Launch a;
-  bool narrow = false;
-  const int st = prepare(pool, pool_pages, physical, physical_stride_q, physical_stride_k, raw,
-                         raw_stride_q, raw_stride_k, lengths, length_stride, n_queries,
-                         selected_k, freqs, freq_rows, native, a, narrow);
-  if (st != RM_OK || !a.out) return st;
-  launch_unpack<kKeep, true>(narrow, a, (hipStream_t)stream);
-  return hipGetLastError() == hipSuccess ? RM_OK : RM_ERR_LAUNCH;
+  return launch_adapter(contiguous(pool), false, page_rows(pool_pages), physical,
+                        physical_stride_q, physical_stride_k, raw, raw_stride_q, raw_stride_k,
+                        lengths, length_stride, n_queries, selected_k, freqs, freq_rows, native,
+                        native_pages, stream);
+}
+
+extern "C" int rm_packed_to_native_planes(const uint8_t* values, const uint64_t* bitmaps,
+                                          const uint8_t* scales, int64_t rows,
+                                          const int32_t* physical, int64_t physical_stride_q,
+                                          int64_t physical_stride_k, const int32_t* raw,
+                                          int64_t raw_stride_q, int64_t raw_stride_k,
+                                          const int32_t* lengths, int64_t length_stride,
+                                          int64_t n_queries, int64_t selected_k,
+                                          const float* freqs, int64_t freq_rows, uint8_t* native,
+                                          int64_t native_pages, void* stream) {
+  return launch_adapter(plane_src(values, bitmaps, scales), true, rows, physical,
+                        physical_stride_q, physical_stride_k, raw, raw_stride_q, raw_stride_k,
+                        lengths, length_stride, n_queries, selected_k, freqs, freq_rows, native,
+                        native_pages, stream);
 }
 
 extern "C" int rm_unpack_gather_bf16(const uint8_t* pool, int64_t pool_pages,

@@ -29,10 +29,29 @@ constexpr int kPageBytes = kPageRecords * kRecordBytes;                       //
 constexpr int kNativeDataBytes = kNopeDim + 2 * (kHeadDim - kNopeDim);       // 576
 constexpr int kNativePageBytes = kPageRecords * (kNativeDataBytes + kScaleBytes);  // 37376
 
+// Where the Packed records of a pool live. Contiguous pages: `values` is the
+// pool; a page holds 64 records back to back, so slot s starts s * (K + 72)
+// bytes in (the other two pointers are unused). Planes (the reference's pool
+// tensors values u8 [rows, K], bitmaps u64 [rows, 8], scales u8 [rows, 8],
+// candidate-sglang.patch:900-904): the three parts of slot s are row s of
+// each plane.
+struct PackedSrc {
+  const uint8_t* values;
+  const uint8_t* bitmaps;
+  const uint8_t* scales;
+};
+struct PackedDst {  // the same, written by the store
+  uint8_t* values;
+  uint8_t* bitmaps;
+  uint8_t* scales;
+};
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
@@ -88,6 +107,58 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// ---- hardware-rounded primitives ----------------------------------------
+// Each equals the software rounding above on its whole input domain; the
+// self-test library (selftest.hip) checks that exhaustively on the GPU.
+
+// Two floats -> packed BF16, round to nearest even (v_cvt_pk_bf16_f32; equal
+// to bf16_rne for every non-NaN input).
+__device__ __forceinline__ bf16x2 bf16_pair(float a, float b) {
+  return bf16x2{(__bf16)a, (__bf16)b};
+}
+
+// E4M3 codes of a BF16 pair divided by a power-of-two scale, RNE, into byte
+// pair 0 (kHi false) or 1 of `acc` (v_cvt_scalef32_pk_fp8_bf16; equal to
+// e4m3_rne(n / scale) for every finite BF16 n with |n / scale| <= 448).
+template <bool kHi>
+__device__ __forceinline__ s16x2 fp8_pair(s16x2 acc, bf16x2 n, float scale) {
+  return __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(acc, n, scale, kHi);
+}
+
+// Two E4M3 codes (bytes 0-1, or 2-3 with kHi) times a power-of-two scale ->
+// two BF16 (v_cvt_scalef32_pk_bf16_fp8; equal to rounding the exact product
+// code * scale to BF16 for every finite code and every UE8M0 scale the store
+// writes).
+template <bool kHi>
+__device__ __forceinline__ uint32_t fp8_pair_to_bf16(uint32_t codes, float scale) {
+  bf16x2 r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(codes, scale, kHi);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// RN(1 / RN(sqrt(x))) for x = sumsq / 512 + eps (wave-uniform). For
+// 2^-96 <= x < 2^128 the root s lies in [2^-48, 2^64), where v_sqrt_f32 is
+// the correctly rounded root and one Newton step from v_rcp_f32,
+// fma(fma(-s, r0, 1), r0, r0), equals __fdiv_rn(1, s); other x take the
+// general sequence.
+__device__ __forceinline__ bool inv_root_fast_range(uint32_t xb) {
+  return xb - 0x0f800000u < 0x7f800000u - 0x0f800000u;
+}
+__device__ __forceinline__ float inv_root_fast(float x) {
+  const float s = __builtin_amdgcn_sqrtf(x);
+  const float r0 = __builtin_amdgcn_rcpf(s);
+  return __builtin_fmaf(__builtin_fmaf(-s, r0, 1.0f), r0, r0);
+}
+__device__ __forceinline__ float inv_root_general(float x) {
+  return __fdiv_rn(1.0f, __fsqrt_rn(x));
+}
+__device__ __forceinline__ float inv_root(float x) {
+  return inv_root_fast_range(__float_as_uint(x)) ? inv_root_fast(x) : inv_root_general(x);
+}
+__device__ __forceinline__ float inv_rms(float sumsq, float eps) {
+  const float x = sumsq * (1.0f / 512.0f) + eps;
+  return inv_root(__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x))));
 }
 
 // Tail rotation of 4 interleaved (re, im) pairs held as floats, with

@@ -1,0 +1,170 @@
+// Self-test kernels: the hardware-rounded primitives of remnant_device.h
+// (the functions the pack, reconstruct and decode kernels call) evaluated over
+// their whole input domains, for the GPU tests to compare with the software
+// rounding and with the CPU oracle. Test infrastructure, built into its own
+// library (libremnant_selftest.so); the product library does not contain it.
+#include "remnant_device.h"
+
+using namespace rm;
+
+namespace {
+
+constexpr int kBlocks = 4096;
+constexpr int kThreads = 256;
+
+// Add a per-thread mismatch count to result[0] (one atomic per wave) and
+// lower result[1] to the smallest mismatching input.
+__device__ void report(unsigned long long* result, unsigned long long bad, uint64_t first_bad) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) bad += __shfl_xor(bad, d, 64);
+  if ((threadIdx.x & 63) == 0 && bad) atomicAdd(result, bad);
+  if (first_bad != ~0ull) atomicMin(result + 1, first_bad);
+}
+
+// FP32 -> BF16 pair conversion vs bf16_rne over inputs [first, first + count).
+__global__ __launch_bounds__(kThreads) void bf16_pair_kernel(uint64_t first, uint64_t count,
+                                                             unsigned long long* result) {
+  unsigned long long bad = 0;
+  uint64_t first_bad = ~0ull;
+  for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; 2 * i < count;
+       i += (uint64_t)gridDim.x * kThreads) {
+    const uint64_t u0 = first + 2 * i, u1 = u0 + 1 < first + count ? u0 + 1 : u0;
+    const float a = u2f((uint32_t)u0), b = u2f((uint32_t)u1);
+    const uint32_t hw = __builtin_bit_cast(uint32_t, bf16_pair(a, b));
+    const bool nan_a = ((uint32_t)u0 & 0x7fffffffu) > 0x7f800000u;
+    const bool nan_b = ((uint32_t)u1 & 0x7fffffffu) > 0x7f800000u;
+    if (!nan_a && (hw & 0xffffu) != bf16_rne(a)) {
+      ++bad;
+      first_bad = first_bad < u0 ? first_bad : u0;
+    }
+    if (!nan_b && u1 != u0 && (hw >> 16) != bf16_rne(b)) {
+      ++bad;
+      first_bad = first_bad < u1 ? first_bad : u1;
+    }
+  }
+  report(result, bad, first_bad);
+}
+
+// Scaled FP8 encode: out[(e - e_lo) * 65536 + n] = code of BF16 pattern n at
+// scale 2^e (byte 0 of the pair conversion; both halves are checked equal).
+__global__ __launch_bounds__(kThreads) void fp8_encode_kernel(int e_lo, int e_count,
+                                                              uint8_t* out,
+                                                              unsigned long long* result) {
+  unsigned long long bad = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < (uint64_t)e_count * 65536;
+       i += (uint64_t)gridDim.x * kThreads) {
+    const int e = e_lo + (int)(i >> 16);
+    const uint16_t n = (uint16_t)(i & 0xffffu);
+    const __bf16 v = __builtin_bit_cast(__bf16, n);
+    s16x2 acc = {0, 0};
+    acc = fp8_pair<false>(acc, bf16x2{v, v}, exp2i(e));
+    acc = fp8_pair<true>(acc, bf16x2{v, v}, exp2i(e));
+    const uint32_t w = __builtin_bit_cast(uint32_t, acc);
+    if ((w & 0xff) != ((w >> 8) & 0xff) || (w & 0xffff) != (w >> 16)) ++bad;
+    out[i] = (uint8_t)(w & 0xffu);
+  }
+  report(result, bad, ~0ull);
+}
+
+// Scaled FP8 decode: out[s * 256 + c] = BF16 bits of code c at scale byte s
+// (2^(s - 127)), s in 1..254 (0 for s = 0 and 255).
+__global__ __launch_bounds__(kThreads) void fp8_decode_kernel(uint16_t* out) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= 256 * 256) return;
+  const int s = i >> 8, c = i & 255;
+  uint16_t r = 0;
+  if (s >= 1 && s <= 254) {
+    const uint32_t codes = (uint32_t)c | ((uint32_t)c << 8);
+    r = (uint16_t)(fp8_pair_to_bf16<false>(codes, exp2i(s - 127)) & 0xffffu);
+  }
+  out[i] = r;
+}
+
+// Fast reciprocal root vs the correctly rounded sequence over FP32 bit
+// patterns [first, end) inside its range.
+__global__ __launch_bounds__(kThreads) void inv_root_kernel(uint32_t first, uint32_t end,
+                                                            unsigned long long* result) {
+  unsigned long long bad = 0;
+  uint64_t first_bad = ~0ull;
+  for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; first + i < end;
+       i += (uint64_t)gridDim.x * kThreads) {
+    const uint32_t xb = first + (uint32_t)i;
+    if (!inv_root_fast_range(xb)) continue;
+    const float x = u2f(xb);
+    if (__float_as_uint(inv_root_fast(x)) != __float_as_uint(inv_root_general(x))) {
+      ++bad;
+      first_bad = first_bad < xb ? first_bad : xb;
+    }
+  }
+  report(result, bad, first_bad);
+}
+
+// Per-element RMS reciprocal of the store: r = RN(1 / RN(sqrt(sumsq / 512 + eps))).
+__global__ __launch_bounds__(kThreads) void inv_rms_kernel(const float* sumsq, const float* eps,
+                                                           float* out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads)
+    out[i] = inv_root(sumsq[i] * (1.0f / 512.0f) + eps[i]);
+}
+
+// The BF16 pair conversion of an array: out[i] = BF16 bits of x[i] (n even).
+__global__ __launch_bounds__(kThreads) void bf16_array_kernel(const float* x, uint32_t* out,
+                                                              int64_t pairs) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < pairs;
+       i += (int64_t)gridDim.x * kThreads)
+    out[i] = __builtin_bit_cast(uint32_t, bf16_pair(x[2 * i], x[2 * i + 1]));
+}
+
+int status() { return hipGetLastError() == hipSuccess ? 0 : -6; }
+
+}  // namespace
+
+// result: device [2] u64, initialised to {0, ~0} by the caller.
+extern "C" int rmt_bf16_pair_mismatches(uint64_t first, uint64_t count,
+                                        unsigned long long* result, void* stream) {
+  if (first + count > (1ull << 32)) return -2;
+  hipLaunchKernelGGL(bf16_pair_kernel, dim3(kBlocks), dim3(kThreads), 0, (hipStream_t)stream,
+                     first, count, result);
+  return status();
+}
+
+// out: device [(e_hi - e_lo + 1) * 65536] u8; result as above (pair halves that differ).
+extern "C" int rmt_fp8_encode_table(int e_lo, int e_hi, uint8_t* out, unsigned long long* result,
+                                    void* stream) {
+  if (e_lo < -126 || e_hi > 127 || e_hi < e_lo) return -2;
+  hipLaunchKernelGGL(fp8_encode_kernel, dim3(kBlocks), dim3(kThreads), 0, (hipStream_t)stream,
+                     e_lo, e_hi - e_lo + 1, out, result);
+  return status();
+}
+
+// out: device [256 * 256] u16.
+extern "C" int rmt_fp8_decode_table(uint16_t* out, void* stream) {
+  hipLaunchKernelGGL(fp8_decode_kernel, dim3(256), dim3(kThreads), 0, (hipStream_t)stream, out);
+  return status();
+}
+
+extern "C" int rmt_inv_root_mismatches(uint32_t first, uint32_t end, unsigned long long* result,
+                                       void* stream) {
+  if (end < first) return -2;
+  hipLaunchKernelGGL(inv_root_kernel, dim3(kBlocks), dim3(kThreads), 0, (hipStream_t)stream,
+                     first, end, result);
+  return status();
+}
+
+extern "C" int rmt_inv_rms(const float* sumsq, const float* eps, float* out, int64_t n,
+                           void* stream) {
+  if (n < 0) return -2;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(inv_rms_kernel, dim3(kBlocks), dim3(kThreads), 0, (hipStream_t)stream,
+                     sumsq, eps, out, n);
+  return status();
+}
+
+// out: device [n] u16 (n even).
+extern "C" int rmt_bf16_array(const float* x, uint16_t* out, int64_t n, void* stream) {
+  if (n < 0 || (n & 1)) return -2;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(bf16_array_kernel, dim3(kBlocks), dim3(kThreads), 0, (hipStream_t)stream, x,
+                     (uint32_t*)out, n / 2);
+  return status();
+}

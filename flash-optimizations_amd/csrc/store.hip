@@ -123,29 +123,10 @@ __device__ __forceinline__ float wave_tree_sum(float p) {
   return lane_value(p, 63);
 }
 
-// r = RN(1 / RN(sqrt(sumsq / 512 + eps))) for the wave-uniform sum. For
-// 2^-96 <= x < 2^128 the root s lies in [2^-48, 2^64), where v_sqrt_f32 is
-// the correctly rounded root (the compiler's __fsqrt_rn applies no scaling
-// there) and one Newton step from v_rcp_f32, fma(fma(-s, r0, 1), r0, r0),
-// equals __fdiv_rn(1, s) for every float s (checked exhaustively on gfx950
-// for all s in that range); other x take the general sequence.
-__device__ __forceinline__ float inv_rms(float sumsq, float eps) {
-  const float x = sumsq * (1.0f / 512.0f) + eps;
-  const uint32_t xb = (uint32_t)__builtin_amdgcn_readfirstlane(__float_as_int(x));
-  if (xb - 0x0f800000u < 0x7f800000u - 0x0f800000u) {
-    const float s = __builtin_amdgcn_sqrtf(__uint_as_float(xb));
-    const float r0 = __builtin_amdgcn_rcpf(s);
-    return __builtin_fmaf(__builtin_fmaf(-s, r0, 1.0f), r0, r0);
-  }
-  return __fdiv_rn(1.0f, __fsqrt_rn(__uint_as_float(xb)));
-}
-
 __device__ __forceinline__ int popc_ballot(bool pred) {
   return __popcll(__ballot(pred));
 }
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 // Inclusive prefix sum of x over the wave's lanes (row shifts within rows of
 // 16, then row broadcasts 15 and 31); the exclusive sum subtracts x.
@@ -369,11 +350,10 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
   return keep;
 }
 
-template <bool kBf16, int kK>
+template <bool kBf16, int kK, bool kPlanes>
 __global__ __launch_bounds__(256) void pack_rows_kernel(
     const void* __restrict__ x, int64_t stride, const float* __restrict__ weight, float eps,
-    const int32_t* __restrict__ slots, int64_t n, uint8_t* __restrict__ pool,
-    int64_t pool_rows) {
+    const int32_t* __restrict__ slots, int64_t n, PackedDst dst_pool, int64_t pool_rows) {
   using R = Rec<kK>;
   __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][R::kSpill + 64];
   // compaction selectors: for a keep byte, byte p of the entry is the slot
@@ -457,7 +437,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     }
     bf16x2 nb[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) nb[i] = bf16x2{(__bf16)y[2 * i], (__bf16)y[2 * i + 1]};
+    for (int i = 0; i < 4; ++i) nb[i] = bf16_pair(y[2 * i], y[2 * i + 1]);
     // group amax: rounding is monotonic, so max |bf16(y)| = bf16(max |y|)
     float ay = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
     ay = fmaxf(ay, fmaxf(fmaxf(fabsf(y[4]), fabsf(y[5])), fmaxf(fabsf(y[6]), fabsf(y[7]))));
@@ -474,10 +454,10 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     // the software encode for every in-range BF16 input); |n / 2^e| <= 448
     const float scale = exp2i(e);
     s16x2 c01 = {0, 0}, c45 = {0, 0};
-    c01 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c01, nb[0], scale, false);
-    c01 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c01, nb[1], scale, true);
-    c45 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c45, nb[2], scale, false);
-    c45 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c45, nb[3], scale, true);
+    c01 = fp8_pair<false>(c01, nb[0], scale);
+    c01 = fp8_pair<true>(c01, nb[1], scale);
+    c45 = fp8_pair<false>(c45, nb[2], scale);
+    c45 = fp8_pair<true>(c45, nb[3], scale);
     const uint32_t lo = __builtin_bit_cast(uint32_t, c01), hi = __builtin_bit_cast(uint32_t, c45);
 
     // compaction: survivors go to [rank, rank + popcount) in coordinate order,
@@ -503,11 +483,24 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     wave_lds_sync();
 
     // the record is 8-byte aligned: one 8-byte store per lane (41 lanes for the
-    // 328-byte record; the 520-byte 448-survivor record needs a 65th piece)
-    uint8_t* dst = pool + (int64_t)(slot >> 6) * R::kPage + (slot & 63) * R::kBytes;
-    if (lane < R::kPieces) *(u32x2*)(dst + 8 * lane) = *(const u32x2*)(st + 8 * lane);
-    if (R::kPieces > 64 && lane < R::kPieces - 64)
-      *(u32x2*)(dst + 512 + 8 * lane) = *(const u32x2*)(st + 512 + 8 * lane);
+    // 328-byte record; the 520-byte 448-survivor record needs a 65th piece).
+    // Contiguous pages hold 64 records back to back (slot s at s * kBytes);
+    // planes take lane pieces 0..K/8-1 (codes), the next 8 (bitmap) and the
+    // one after them (scales) at row `slot` of their plane.
+    if (kPlanes) {
+      uint8_t* dst = lane < kK / 8 ? dst_pool.values + (int64_t)slot * kK + 8 * lane
+                     : lane < kK / 8 + 8
+                         ? dst_pool.bitmaps + (int64_t)slot * kBitmapBytes + 8 * (lane - kK / 8)
+                         : dst_pool.scales + (int64_t)slot * kScaleBytes;
+      if (lane < R::kPieces) *(u32x2*)dst = *(const u32x2*)(st + 8 * lane);
+      if (R::kPieces > 64 && lane == 0)
+        *(u32x2*)(dst_pool.scales + (int64_t)slot * kScaleBytes) = *(const u32x2*)(st + 512);
+    } else {
+      uint8_t* dst = dst_pool.values + (int64_t)slot * R::kBytes;
+      if (lane < R::kPieces) *(u32x2*)(dst + 8 * lane) = *(const u32x2*)(st + 8 * lane);
+      if (R::kPieces > 64 && lane < R::kPieces - 64)
+        *(u32x2*)(dst + 512 + 8 * lane) = *(const u32x2*)(st + 512 + 8 * lane);
+    }
     wave_lds_sync();
   }
 }
@@ -598,15 +591,67 @@ int grid_for(int64_t n) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-template <int kK>
-void launch_pack(bool bf16, const void* x, int64_t stride, const float* weight, float eps,
-                 const int32_t* slots, int64_t n, uint8_t* pool, int64_t rows, hipStream_t s) {
-  if (bf16)
-    hipLaunchKernelGGL((pack_rows_kernel<true, kK>), dim3(grid_for(n)), dim3(256), 0, s, x,
-                       stride, weight, eps, slots, n, pool, rows);
+struct PackLaunch {
+  bool bf16, planes;
+  const void* x;
+  int64_t stride;
+  const float* weight;
+  float eps;
+  const int32_t* slots;
+  int64_t n;
+  PackedDst pool;
+  int64_t rows;
+  hipStream_t stream;
+};
+
+template <int kK, bool kPlanes>
+void launch_pack_layout(const PackLaunch& L) {
+  if (L.bf16)
+    hipLaunchKernelGGL((pack_rows_kernel<true, kK, kPlanes>), dim3(grid_for(L.n)), dim3(256), 0,
+                       L.stream, L.x, L.stride, L.weight, L.eps, L.slots, L.n, L.pool, L.rows);
   else
-    hipLaunchKernelGGL((pack_rows_kernel<false, kK>), dim3(grid_for(n)), dim3(256), 0, s, x,
-                       stride, weight, eps, slots, n, pool, rows);
+    hipLaunchKernelGGL((pack_rows_kernel<false, kK, kPlanes>), dim3(grid_for(L.n)), dim3(256), 0,
+                       L.stream, L.x, L.stride, L.weight, L.eps, L.slots, L.n, L.pool, L.rows);
+}
+
+template <int kK>
+void launch_pack(const PackLaunch& L) {
+  if (L.planes)
+    launch_pack_layout<kK, true>(L);
+  else
+    launch_pack_layout<kK, false>(L);
+}
+
+// Argument checks and launch shared by the store entry points. Contiguous
+// pools are 16-byte aligned, planes 8-byte aligned.
+int pack_any(const void* x, int x_dtype, int64_t x_row_stride, const float* weight, float eps,
+             const int32_t* dst_slot, int64_t n, PackedDst pool, bool planes, int64_t rows,
+             int keep_count, void* stream) {
+  if (n < 0 || rows < 0) return RM_ERR_SHAPE;
+  if (keep_count < 64 || keep_count > 448 || keep_count % 64) return RM_ERR_SHAPE;
+  if (n == 0) return RM_OK;
+  if (!x || !weight || !dst_slot || !pool.values || (planes && (!pool.bitmaps || !pool.scales)))
+    return RM_ERR_NULL;
+  if (x_dtype != RM_F32 && x_dtype != RM_BF16) return RM_ERR_DTYPE;
+  if (x_row_stride < kHeadDim && n > 1) return RM_ERR_SHAPE;
+  const int esize = x_dtype == RM_BF16 ? 2 : 4;
+  if (!aligned(x, 16) || ((x_row_stride * esize) & 15) || !aligned(weight, 16))
+    return RM_ERR_ALIGN;
+  if (planes ? !(aligned(pool.values, 8) && aligned(pool.bitmaps, 8) && aligned(pool.scales, 8))
+             : !aligned(pool.values, 16))
+    return RM_ERR_ALIGN;
+  const PackLaunch L{x_dtype == RM_BF16, planes, x, x_row_stride, weight, eps, dst_slot, n,
+                     pool, rows, (hipStream_t)stream};
+  switch (keep_count) {
+    case 64: launch_pack<64>(L); break;
+    case 128: launch_pack<128>(L); break;
+    case 192: launch_pack<192>(L); break;
+    case 256: launch_pack<256>(L); break;
+    case 320: launch_pack<320>(L); break;
+    case 384: launch_pack<384>(L); break;
+    default: launch_pack<448>(L); break;
+  }
+  return hipGetLastError() == hipSuccess ? RM_OK : RM_ERR_LAUNCH;
 }
 
 }  // namespace
@@ -622,29 +667,19 @@ extern "C" int rm_pack_rows_k(const void* x, int x_dtype, int64_t x_row_stride,
                               const float* weight, float eps, const int32_t* dst_slot,
                               int64_t n, uint8_t* pool, int64_t pool_pages, int keep_count,
                               void* stream) {
-  if (n < 0 || pool_pages < 0) return RM_ERR_SHAPE;
-  if (keep_count < 64 || keep_count > 448 || keep_count % 64) return RM_ERR_SHAPE;
-  if (n == 0) return RM_OK;
-  if (!x || !weight || !dst_slot || !pool) return RM_ERR_NULL;
-  if (x_dtype != RM_F32 && x_dtype != RM_BF16) return RM_ERR_DTYPE;
-  if (x_row_stride < kHeadDim && n > 1) return RM_ERR_SHAPE;
-  const int esize = x_dtype == RM_BF16 ? 2 : 4;
-  if (!aligned(x, 16) || ((x_row_stride * esize) & 15) || !aligned(weight, 16) ||
-      !aligned(pool, 16))
-    return RM_ERR_ALIGN;
-  hipStream_t s = (hipStream_t)stream;
-  const int64_t rows = pool_pages * kPageRecords;
-  const bool bf16 = x_dtype == RM_BF16;
-  switch (keep_count) {
-    case 64: launch_pack<64>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
-    case 128: launch_pack<128>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
-    case 192: launch_pack<192>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
-    case 256: launch_pack<256>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
-    case 320: launch_pack<320>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
-    case 384: launch_pack<384>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
-    default: launch_pack<448>(bf16, x, x_row_stride, weight, eps, dst_slot, n, pool, rows, s); break;
-  }
-  return hipGetLastError() == hipSuccess ? RM_OK : RM_ERR_LAUNCH;
+  if (pool_pages < 0 || pool_pages > ((int64_t)1 << 25)) return RM_ERR_SHAPE;  // int32 slots
+  return pack_any(x, x_dtype, x_row_stride, weight, eps, dst_slot, n,
+                  PackedDst{pool, nullptr, nullptr}, false, pool_pages * kPageRecords,
+                  keep_count, stream);
+}
+
+extern "C" int rm_pack_rows_planes(const void* x, int x_dtype, int64_t x_row_stride,
+                                   const float* weight, float eps, const int32_t* dst_slot,
+                                   int64_t n, uint8_t* values, uint64_t* bitmaps,
+                                   uint8_t* scales, int64_t rows, int keep_count, void* stream) {
+  if (rows > ((int64_t)1 << 31)) return RM_ERR_SHAPE;  // int32 slots
+  return pack_any(x, x_dtype, x_row_stride, weight, eps, dst_slot, n,
+                  PackedDst{values, (uint8_t*)bitmaps, scales}, true, rows, keep_count, stream);
 }
 
 extern "C" int rm_native_store_rows(const void* x, int x_dtype, int64_t x_row_stride,

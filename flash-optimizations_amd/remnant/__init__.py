@@ -8,16 +8,17 @@ decode, each a hand-written gfx950 HIP kernel reached through the C ABI in
 
 from . import config
 from .config import configure_cache_format, packed_profile
-from .flash_mla import (get_decode_metadata, native_sparse_decode_fwd,
+from .flash_mla import (get_decode_metadata, native_sparse_decode_fwd, remnant_buffers,
                         remnant_sparse_decode_fwd, sparse_decode_fwd)
-from .packed import (native_store_rows, pack_rows_fused, packed_to_native, unpack_gather_bf16,
-                     unpack_rows)
+from .packed import (RemnantBuffers, native_store_rows, pack_rows_fused, packed_to_native,
+                     unpack_gather_bf16, unpack_rows)
 from .host_cache import HostLatentPool, copy_records
 from .pool import LatentPool, records_fitting
 
 __all__ = [
     "config", "configure_cache_format", "packed_profile", "get_decode_metadata",
     "native_sparse_decode_fwd", "remnant_sparse_decode_fwd", "sparse_decode_fwd",
+    "remnant_buffers", "RemnantBuffers",
     "native_store_rows", "pack_rows_fused", "packed_to_native", "unpack_gather_bf16",
     "unpack_rows",
     "LatentPool", "records_fitting", "HostLatentPool", "copy_records",

@@ -30,8 +30,19 @@ SIGNATURES = {
     "rm_version": (_i32, []),
     "rm_pack_rows": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _vp, _i64, _vp]),
     "rm_pack_rows_k": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _vp, _i64, _i32, _vp]),
+    "rm_pack_rows_planes": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _vp, _vp, _vp, _i64,
+                                   _i32, _vp]),
     "rm_native_store_rows": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _vp,
                                     _i64, _vp]),
+    "rm_unpack_gather_bf16_planes": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i64, _vp,
+                                            _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp,
+                                            _vp]),
+    "rm_packed_to_native_planes": (_i32, [_vp, _vp, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
+                                          _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "rm_remnant_sparse_decode_planes_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64,
+                                                   _vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp,
+                                                   _i64, _vp, _i64, _vp, _vp, _vp, _i64, _f32,
+                                                   _vp, _vp, _vp, _sz, _vp]),
     "rm_unpack_gather_bf16": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
                                      _i64, _i64, _vp, _i64, _vp, _vp]),
     "rm_unpack_gather_bf16_k": (_i32, [_vp, _i64, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp,

@@ -24,7 +24,7 @@ import math
 import torch
 
 from . import _lib, config
-from .packed import _as_pool, _check_cuda, _stream
+from .packed import RemnantBuffers, _as_pool, _as_source, _check_cuda, _plane_buffers, _stream
 
 
 def get_decode_metadata(tokens: int, heads: int, topk: int, swa_topk: int = 0) -> tuple[int, int]:
@@ -61,10 +61,30 @@ def _swa_args(swa_pool, swa_indices, swa_lengths, batch, q_len):
     return sbuf, swa_indices, swa_lengths, width
 
 
+def remnant_buffers(values, bitmaps=None, scales=None, *, layer_id=None) -> RemnantBuffers:
+    """The Packed record source a Direct decode reads (the binding's
+    ``remnant_buffers``, Dockerfile.v0.5.18:56): the reference's pool planes
+    ``remnant_buffers(values, bitmaps, scales)`` (values u8 [rows, 256],
+    bitmaps u64 [rows, 8], scales u8 [rows, 8]), a ``(values, bitmaps,
+    scales)`` tuple, a ``LatentPool`` (with ``layer_id``) or a uint8 page
+    tensor. The result is accepted wherever a pool is: by
+    ``remnant_sparse_decode_fwd``, ``unpack_gather_bf16``, ``pack_rows_fused``
+    and ``packed_to_native``."""
+    if bitmaps is not None or scales is not None:
+        if bitmaps is None or scales is None:
+            raise ValueError("remnant_buffers takes values, bitmaps and scales together")
+        return _plane_buffers(values, bitmaps, scales)
+    src, packed, _ = _as_source(values, layer_id)
+    if not packed:
+        raise ValueError("remnant_buffers describes a Packed pool")
+    return src
+
+
 def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length, sink,
             freqs_cis, softmax_scale, out, lse, workspace, layer_id, swa_pool=None,
             swa_indices=None, swa_lengths=None):
-    buf, is_packed, keep = _as_pool(pool, layer_id)
+    src, is_packed, keep = _as_source(pool, layer_id)
+    buf = src if not is_packed else None
     if is_packed != packed:
         raise ValueError("pool format does not match the decode reader")
     if packed and keep != config.KEEP_COUNT:
@@ -120,12 +140,26 @@ def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length
         raise ValueError("workspace must be a contiguous uint8 tensor on the GPU")
     if need and (workspace is None or workspace.numel() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
-    _check_cuda(q, buf, block_table, indices, seqlens, topk_length, sink, freqs_cis, out, lse,
-                sbuf, sidx, slen, workspace)
+    if packed and src.planes and src.rows % 2:
+        raise ValueError("plane buffers need an even number of rows")
+    pool_tensors = src.tensors() if packed else (buf,)
+    _check_cuda(q, *pool_tensors, block_table, indices, seqlens, topk_length, sink, freqs_cis,
+                out, lse, sbuf, sidx, slen, workspace)
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     ws_ptr = ptr(workspace) if need else None
     ws_bytes = workspace.numel() * workspace.element_size() if need else 0
     lib = _lib.load()
+    if packed and src.planes:
+        _lib.check(lib.rm_remnant_sparse_decode_planes_fwd(
+            q.data_ptr(), batch, q_len, heads, src.values.data_ptr(), src.bitmaps.data_ptr(),
+            src.scales.data_ptr(), src.rows, block_table.data_ptr(), bt_stride,
+            block_table.shape[1], ptr(seqlens), indices.data_ptr(), topk, ptr(topk_length),
+            ptr(sbuf), 0 if sbuf is None else sbuf.shape[0], ptr(sidx), width, ptr(slen),
+            ptr(sink), freq_ptr, freq_rows, float(softmax_scale), out.data_ptr(), lse.data_ptr(),
+            ws_ptr, ws_bytes, _stream()), "rm_remnant_sparse_decode_planes_fwd")
+        return out, lse
+    if packed:
+        buf = src.pages
     if width > 0:
         common = (q.data_ptr(), batch, q_len, heads, buf.data_ptr(), buf.shape[0],
                   block_table.data_ptr(), bt_stride, block_table.shape[1], ptr(seqlens),

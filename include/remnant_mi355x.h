@@ -50,11 +50,24 @@
  *                             (configure_cache_format(..., keep_count=K) with the
  *                             KEEP_K Triton kernels: candidate-sglang.patch:471-479,
  *                             707-736, 775-790; docs/agents/numerical-and-validation.md:10-14)
+ *   rm_pack_rows_planes / rm_unpack_gather_bf16_planes / rm_packed_to_native_planes /
+ *   rm_remnant_sparse_decode_planes_fwd
+ *                             the same operators on the reference's plane-form pool
+ *                             buffers (values, bitmaps, scales): packed.py::_as_buffers
+ *                             and the callers passing the plane tuple
+ *                             (candidate-sglang.patch:782-789, 839, 900-911); the decode
+ *                             side of sgl_kernel/flash_mla.py::remnant_buffers
+ *                             (Dockerfile.v0.5.18:56)
  *
  * Survivor profiles: a Packed pool may instead hold records with K survivors,
  * K = 64..448 in steps of 64: K E4M3 codes, the same 64 bitmap bytes and 8 scale
  * bytes (K + 72 bytes, 8-byte aligned), 64 records per page (64 * (K + 72) B).
  * The sparse decode reads the 256-survivor format only.
+ *
+ * Plane form: the same records held as three row-aligned planes, slot s being
+ * row s of each: values [rows, K] u8 (codes, ascending coordinate), bitmaps
+ * [rows, 8] u64 (the bitmap words as above) and scales [rows, 8] u8. Byte for
+ * byte the record is values row + bitmaps row + scales row.
  */
 #ifndef REMNANT_MI355X_H
 #define REMNANT_MI355X_H
@@ -112,6 +125,14 @@ int rm_pack_rows_k(const void* x, int x_dtype, int64_t x_row_stride, const float
                    float eps, const int32_t* dst_slot, int64_t n, uint8_t* pool,
                    int64_t pool_pages, int keep_count, void* stream);
 
+/* rm_pack_rows_k writing plane-form buffers: record dst_slot[i] goes to row
+ * dst_slot[i] of each plane (a slot < 0 or >= rows is skipped). Planes 8-byte
+ * aligned. */
+int rm_pack_rows_planes(const void* x, int x_dtype, int64_t x_row_stride, const float* weight,
+                        float eps, const int32_t* dst_slot, int64_t n, uint8_t* values,
+                        uint64_t* bitmaps, uint8_t* scales, int64_t rows, int keep_count,
+                        void* stream);
+
 /* Native control store: unpruned RMSNorm, 7 NoPE groups as UE8M0/E4M3, tail
  * rotated with freqs row position[i] * 4 (freqs: [freq_rows, 32] complex64 as
  * interleaved f32 (cos, sin); NULL = no rotation). Rows whose slot is out of
@@ -143,6 +164,17 @@ int rm_unpack_gather_bf16_k(const uint8_t* pool, int64_t pool_pages, int keep_co
                             int64_t selected_k, const float* freqs, int64_t freq_rows,
                             uint16_t* out, void* stream);
 
+/* rm_unpack_gather_bf16_k reading plane-form buffers of `rows` records
+ * (physical entries are plane rows). Planes 8-byte aligned. */
+int rm_unpack_gather_bf16_planes(const uint8_t* values, const uint64_t* bitmaps,
+                                 const uint8_t* scales, int64_t rows, int keep_count,
+                                 const int32_t* physical, int64_t physical_stride_q,
+                                 int64_t physical_stride_k, const int32_t* raw,
+                                 int64_t raw_stride_q, int64_t raw_stride_k,
+                                 const int32_t* lengths, int64_t length_stride, int64_t n_queries,
+                                 int64_t selected_k, const float* freqs, int64_t freq_rows,
+                                 uint16_t* out, void* stream);
+
 /* Adapter: the rows rm_unpack_gather_bf16 would produce (same gather,
  * validity and RoPE rules; invalid rows are zero rows), each re-encoded as a
  * Native 584-byte record (seven UE8M0/E4M3 NoPE groups from the row's own
@@ -156,6 +188,15 @@ int rm_packed_to_native(const uint8_t* pool, int64_t pool_pages, const int32_t* 
                         const int32_t* lengths, int64_t length_stride, int64_t n_queries,
                         int64_t selected_k, const float* freqs, int64_t freq_rows,
                         uint8_t* native, int64_t native_pages, void* stream);
+
+/* rm_packed_to_native reading plane-form buffers (values [rows, 256]). */
+int rm_packed_to_native_planes(const uint8_t* values, const uint64_t* bitmaps,
+                               const uint8_t* scales, int64_t rows, const int32_t* physical,
+                               int64_t physical_stride_q, int64_t physical_stride_k,
+                               const int32_t* raw, int64_t raw_stride_q, int64_t raw_stride_k,
+                               const int32_t* lengths, int64_t length_stride, int64_t n_queries,
+                               int64_t selected_k, const float* freqs, int64_t freq_rows,
+                               uint8_t* native, int64_t native_pages, void* stream);
 
 /* Record transfer between two pools of one format (host-cache backup and
  * restore): for i < n and every layer l < layers, record src_slots[i] of layer
@@ -199,6 +240,21 @@ int rm_remnant_sparse_decode_fwd(const uint16_t* q, int64_t batch, int64_t q_len
                                  const float* freqs, int64_t freq_rows, float softmax_scale,
                                  uint16_t* out, float* lse, void* workspace,
                                  size_t workspace_bytes, void* stream);
+
+/* rm_remnant_sparse_decode_swa_fwd on plane-form buffers of pool_rows
+ * 256-survivor records (values [rows, 256], bitmaps [rows, 8], scales [rows, 8];
+ * pool_rows even, each plane 16-byte aligned): logical record r of request b
+ * is plane row block_table[b, r / 64] * 64 + r % 64. swa_topk == 0 attends
+ * the C4 list only (the window arguments may then be NULL). */
+int rm_remnant_sparse_decode_planes_fwd(
+    const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads, const uint8_t* values,
+    const uint64_t* bitmaps, const uint8_t* scales, int64_t pool_rows,
+    const int32_t* block_table, int64_t block_table_stride, int64_t max_blocks,
+    const int32_t* seqlens, const int32_t* indices, int64_t topk, const int32_t* topk_length,
+    const uint8_t* swa_pool, int64_t swa_pool_pages, const int32_t* swa_indices,
+    int64_t swa_topk, const int32_t* swa_length, const float* sink, const float* freqs,
+    int64_t freq_rows, float softmax_scale, uint16_t* out, float* lse, void* workspace,
+    size_t workspace_bytes, void* stream);
 
 /* Native control decode: same contract on 584-byte records (tail already rotated). */
 int rm_native_sparse_decode_fwd(const uint16_t* q, int64_t batch, int64_t q_len,

@@ -79,6 +79,9 @@ def lib():
         _lib.orc_unpack_gather_k.argtypes = [vp, i64, ctypes.c_int, vp, i64, i64, vp, i64,
                                              i64, vp, i64, i64, i64, vp, i64, vp]
         _lib.orc_normalize.argtypes = [vp, vp, vp, f32, vp]
+        _lib.orc_e4m3_encode_n.argtypes = [vp, i64, vp]
+        _lib.orc_e4m3_dequant_n.argtypes = [vp, vp, i64, vp]
+        _lib.orc_rms_scale_n.argtypes = [vp, vp, i64, vp]
         _lib.orc_simulate_rows.argtypes = [vp, vp, vp, f32, i64, vp]
         _lib.orc_pack_row.argtypes = [vp, vp, f32, vp, vp, vp, vp]
         _lib.orc_pack_rows_paged.argtypes = [vp, vp, f32, vp, i64, vp, i64]
@@ -142,6 +145,32 @@ def e4m3_decode(code: int) -> float:
 
 def ue8m0_exponent(amax: float) -> int:
     return int(lib().orc_ue8m0_exponent(float(amax)))
+
+
+def e4m3_encode_array(q) -> np.ndarray:
+    """E4M3 codes (RNE) of float32 values with |q| <= 448."""
+    q = _c(q, np.float32).ravel()
+    out = np.zeros(q.shape, np.uint8)
+    lib().orc_e4m3_encode_n(_p(q), q.size, _p(out))
+    return out
+
+
+def e4m3_dequant_array(codes, scale_bytes) -> np.ndarray:
+    """BF16 bits of code * 2^(scale_byte - 127) (the unpack's dequantisation)."""
+    codes, sb = np.broadcast_arrays(_c(codes, np.uint8), _c(scale_bytes, np.uint8))
+    codes, sb = _c(codes, np.uint8).ravel(), _c(sb, np.uint8).ravel()
+    out = np.zeros(codes.shape, np.uint16)
+    lib().orc_e4m3_dequant_n(_p(codes), _p(sb), codes.size, _p(out))
+    return out
+
+
+def rms_scale_array(sumsq, eps) -> np.ndarray:
+    """r = RN(1 / RN(sqrt(sumsq / 512 + eps))) elementwise."""
+    sumsq, eps = np.broadcast_arrays(_c(sumsq, np.float32), _c(eps, np.float32))
+    sumsq, eps = _c(sumsq, np.float32).ravel(), _c(eps, np.float32).ravel()
+    out = np.zeros(sumsq.shape, np.float32)
+    lib().orc_rms_scale_n(_p(sumsq), _p(eps), sumsq.size, _p(out))
+    return out
 
 
 # ---- rows ------------------------------------------------------------------

@@ -153,6 +153,24 @@ float orc_rms_scale(float sumsq, float eps) {
     return 1.0f / s;
 }
 
+/* Array forms of the scalar steps, for the checks of the GPU's hardware
+ * rounding against this oracle over whole input domains. */
+void orc_e4m3_encode_n(const float* q, int64_t n, uint8_t* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_e4m3_encode(q[i]);
+}
+
+/* BF16 of code * 2^(scale_byte - 127), as the unpack computes it. */
+void orc_e4m3_dequant_n(const uint8_t* codes, const uint8_t* scale_bytes, int64_t n,
+                        uint16_t* out) {
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = orc_f32_to_bf16(orc_e4m3_decode(codes[i]) *
+                                 ldexpf(1.0f, (int)scale_bytes[i] - 127));
+}
+
+void orc_rms_scale_n(const float* sumsq, const float* eps, int64_t n, float* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_rms_scale(sumsq[i], eps[i]);
+}
+
 /* Masked RMSNorm -> BF16 (keep may be NULL for the unmasked Native norm). */
 void orc_normalize(const float* x, const uint8_t* keep, const float* w, float eps,
                    uint16_t* n) {

@@ -473,3 +473,126 @@ def test_survivor_profile_pools():
                                           bt, idx)
     hbm = 288 * 10**9
     assert remnant.records_fitting(hbm, "direct", 64) > remnant.records_fitting(hbm, "direct")
+
+
+class _RecordingLib:
+    """Stands for the C library: records which entry point a call reaches."""
+
+    def __init__(self):
+        self.calls = []
+
+    def __getattr__(self, name):
+        if not name.startswith("rm_"):
+            raise AttributeError(name)
+        return lambda *args: self.calls.append((name, args)) or 0
+
+
+def test_bf16_reader_dispatch_plane_buffers_and_empty_inputs(monkeypatch):
+    """Mirror of the reference's test_bf16_reader_opt_in_dispatch_and_empty_inputs
+    (candidate-sglang.patch:896-930): the reference's plane tuple (values u8
+    [rows, 256], bitmaps u64 [rows, 8], scales u8 [rows, 8]) reaches the plane
+    reader with its row count and survivor count, a page tensor the paged
+    reader; fused_rope True and False both take the one fused launch; empty
+    selections launch nothing; a non-bool flag raises TypeError."""
+    from remnant import packed as packed_mod
+    rec = _RecordingLib()
+    monkeypatch.setattr(_lib, "load", lambda: rec)
+    monkeypatch.setattr(packed_mod, "_check_cuda", lambda *t: None)
+    monkeypatch.setattr(packed_mod, "_stream", lambda: 0)
+    buffers = (torch.zeros((1, 256), dtype=torch.uint8), torch.zeros((1, 8), dtype=torch.uint64),
+               torch.zeros((1, 8), dtype=torch.uint8))
+    index = torch.zeros((1, 1), dtype=torch.int32)
+    lengths = torch.ones(1, dtype=torch.int32)
+    freqs = torch.ones((16, 32), dtype=torch.complex64)
+    output = torch.empty((1, 512), dtype=torch.bfloat16)
+    remnant.unpack_gather_bf16(buffers, index, index, lengths, freqs, output)
+    remnant.unpack_gather_bf16(buffers, index, index, lengths, freqs, output, fused_rope=True)
+    assert [c[0] for c in rec.calls] == ["rm_unpack_gather_bf16_planes"] * 2
+    args = rec.calls[0][1]
+    assert args[:3] == tuple(t.data_ptr() for t in buffers) and args[3:5] == (1, 256)
+    # ..., n_queries, selected_k, freqs, freq_rows, output, stream
+    assert args[-6:-2] == (1, 1, freqs.data_ptr(), 16) and args[-2] == output.data_ptr()
+    rec.calls.clear()
+    pages = torch.zeros((2, config.PACKED_PAGE_BYTES), dtype=torch.uint8)
+    remnant.unpack_gather_bf16(pages, index, index, lengths, freqs, output, fused_rope=True)
+    assert [c[0] for c in rec.calls] == ["rm_unpack_gather_bf16_k"]
+    assert rec.calls[0][1][:3] == (pages.data_ptr(), 2, 256)
+    rec.calls.clear()
+    for physical, raw, active in ((index[:0], index[:0], lengths[:0]),
+                                  (index[:, :0], index[:, :0], lengths)):
+        remnant.unpack_gather_bf16(buffers, physical, raw, active, freqs, output,
+                                   fused_rope=True)
+    assert rec.calls == []
+    for invalid in (1, 0, "fused", None):
+        with pytest.raises(TypeError, match="fused_rope must be a bool"):
+            remnant.unpack_gather_bf16(buffers, index, index, lengths, freqs, output,
+                                       fused_rope=invalid)
+    # the store and the Adapter take the same plane tuple
+    x = torch.zeros((1, 512))
+    remnant.pack_rows_fused(x, torch.ones(512), 1e-6, torch.zeros(1, dtype=torch.int32), buffers)
+    native = remnant.LatentPool(1, fmt="native", device="cpu")
+    remnant.packed_to_native(buffers, index, index, lengths, freqs, native)
+    assert [c[0] for c in rec.calls] == ["rm_pack_rows_planes", "rm_packed_to_native_planes"]
+    assert rec.calls[0][1][7:12] == (*(t.data_ptr() for t in buffers), 1, 256)[:5]
+
+
+def test_plane_buffer_validation_and_remnant_buffers():
+    rows = 6
+    v = torch.zeros((rows, 192), dtype=torch.uint8)
+    b = torch.zeros((rows, 8), dtype=torch.uint64)
+    s = torch.zeros((rows, 8), dtype=torch.uint8)
+    rb = remnant.remnant_buffers(v, b, s)
+    assert isinstance(rb, remnant.RemnantBuffers) and rb.planes
+    assert (rb.rows, rb.keep_count) == (rows, 192)
+    assert remnant.remnant_buffers((v, b.view(torch.uint8), s)).keep_count == 192  # u8 view
+    pool = remnant.LatentPool(2, layers=2, device="cpu")
+    pb = remnant.remnant_buffers(pool, layer_id=1)
+    assert not pb.planes and pb.pages.data_ptr() == pool.layer(1).data_ptr() and pb.rows == 128
+    for bad in ((v[:, :100], b, s), (v.float(), b, s), (v, b[:5], s), (v, b.float(), s),
+                (v, b, s[:, :4]), (v, b, s.t().contiguous().t()), (v[:, ::2], b, s),
+                (torch.zeros((rows, 512), dtype=torch.uint8), b, s)):
+        with pytest.raises(ValueError):
+            remnant.unpack_gather_bf16(bad, torch.zeros((1, 1), dtype=torch.int32), None,
+                                       torch.ones(1, dtype=torch.int32), None,
+                                       torch.empty((1, 512), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="together"):
+        remnant.remnant_buffers(v, b)
+    with pytest.raises(ValueError, match="Packed"):
+        remnant.remnant_buffers(remnant.LatentPool(1, fmt="native", device="cpu"))
+    # the Direct decode reads 256-survivor planes with an even row count
+    q = torch.zeros((1, 1, 16, 512), dtype=torch.bfloat16)
+    bt = torch.zeros((1, 1), dtype=torch.int32)
+    idx = torch.zeros((1, 1, 4), dtype=torch.int32)
+    with pytest.raises(ValueError, match="256-survivor"):
+        remnant.remnant_sparse_decode_fwd(q, rb, bt, idx)
+    odd = remnant.remnant_buffers(torch.zeros((5, 256), dtype=torch.uint8),
+                                  torch.zeros((5, 8), dtype=torch.uint64),
+                                  torch.zeros((5, 8), dtype=torch.uint8))
+    with pytest.raises(ValueError, match="even"):
+        remnant.remnant_sparse_decode_fwd(q, odd, bt, idx)
+    # C ABI: null planes, alignment, odd rows
+    lib = _lib.load()
+    _, xq = buf(16384)
+    _, vp = buf(4096)
+    _, bp = buf(1024)
+    _, sp = buf(256)
+    _, ix = buf(64)
+    _, f = buf(256)
+    _, out = buf(2048)
+    assert lib.rm_unpack_gather_bf16_planes(vp, None, sp, 4, 256, ix, 1, 1, None, 0, 0, ix, 1, 1,
+                                            1, None, 0, out, None) == -1
+    assert lib.rm_unpack_gather_bf16_planes(vp, bp + 4, sp, 4, 256, ix, 1, 1, None, 0, 0, ix, 1,
+                                            1, 1, None, 0, out, None) == -3
+    assert lib.rm_unpack_gather_bf16_planes(vp, bp, sp, 4, 200, ix, 1, 1, None, 0, 0, ix, 1, 1,
+                                            1, None, 0, out, None) == -2
+    assert lib.rm_pack_rows_planes(xq, 1, 512, f, 1e-6, ix, 1, vp, None, sp, 4, 256, None) == -1
+    assert lib.rm_pack_rows_planes(xq, 1, 512, f, 1e-6, ix, 1, vp + 4, bp, sp, 4, 256,
+                                   None) == -3
+    dec = [xq, 1, 1, 16, vp, bp, sp, 5, ix, 4, 4, None, ix, 4, None, None, 0, None, 0, None,
+           None, None, 0, 0.1, out, f, None, 0, None]
+    assert lib.rm_remnant_sparse_decode_planes_fwd(*dec) == -2  # odd rows
+    dec[7] = 4
+    dec[5] = bp + 8
+    assert lib.rm_remnant_sparse_decode_planes_fwd(*dec) == -3  # bitmaps not 16-byte aligned
+    dec[5] = None
+    assert lib.rm_remnant_sparse_decode_planes_fwd(*dec) == -1

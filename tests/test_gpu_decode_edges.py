@@ -1,0 +1,405 @@
+"""GPU parity at the edges the shared parity suite leaves open.
+
+* Capacity decode (batch 128 x 2 query tokens, top-k 2048, 32,768-record
+  contexts) on a pool of 450,000 pages (9.4 GB), so record offsets pass 2^32:
+  sampled requests against the oracle, plus pack and reconstruct at the high
+  slots.
+* Realistic logit spread (q scaled so logits have a standard deviation of
+  about 4) at the batch-1 and batch-64 shapes, checked per (token, head):
+  max-abs <= 2e-2 and cosine >= 0.9999 for every row, not only overall.
+* Extreme bitmaps (empty words, full words, survivors only in words 0-3 or
+  4-7, fully pruned groups with scale byte 105, the reference's tie rows)
+  through pack, reconstruct (bit-exact) and the Direct decode
+  (scripts/modal/kernels.py:286-287 "bitmap-edges").
+* The Direct decode captured in a HIP graph and replayed after q, indices,
+  lengths and records change in place (kernels.py:288-289 graph replay).
+* The Native store with FP32 input; the batched decode at 4k-128k-token
+  contexts (up to 32,768 records).
+* FP32-input pack with full-precision mantissas near the threshold and exact
+  ties, on many records per wave (the histogram levels of the threshold search).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import remnant
+from remnant import synthetic as syn
+from test_gpu_parity import (COS_MIN, DEV, OUT_TOL, W1, assert_pool_equal, build_decode_case,
+                             check_decode, gpu_pack, oracle_decode, oracle_pack, run_decode)
+
+pytestmark = pytest.mark.gpu
+
+
+def banner(msg):
+    print(f"[gpu-edges] {msg}", flush=True)
+
+
+def per_row_check(out, ref, lse=None, ref_lse=None):
+    """Tolerance per (token, head) row of [.., 512] outputs."""
+    o = out.reshape(-1, 512).astype(np.float64)
+    r = ref.reshape(-1, 512).astype(np.float64)
+    err = np.abs(o - r).max(axis=1)
+    assert err.max() <= OUT_TOL, f"row {int(err.argmax())}: max-abs {err.max()}"
+    no, nr = np.linalg.norm(o, axis=1), np.linalg.norm(r, axis=1)
+    live = (no > 0) | (nr > 0)
+    cos = (o * r).sum(axis=1)[live] / np.maximum(no * nr, 1e-300)[live]
+    assert cos.min() >= COS_MIN, f"row {int(np.nonzero(live)[0][cos.argmin()])}: cosine {cos.min()}"
+    if lse is not None:
+        finite = np.isfinite(ref_lse)
+        assert np.array_equal(finite, np.isfinite(lse))
+        assert np.abs(lse[finite] - ref_lse[finite]).max() <= OUT_TOL
+    return float(err.max()), float(cos.min())
+
+
+# ---- realistic logit spread, per (token, head) ----------------------------------------------
+
+@pytest.mark.parametrize("shape", ["b1", "b64"])
+@pytest.mark.parametrize("packed", [True, False], ids=["direct", "native"])
+def test_decode_realistic_logit_spread_per_head(shape, packed):
+    """q scaled so that the logits q.K / sqrt(512) have std ~4 (unit-RMS rows):
+    a few records carry most of each softmax, so the output is far from the
+    near-uniform average a small q gives, and every (token, head) row must meet
+    the bar on its own."""
+    banner(f"decode logit spread {shape} packed={packed}")
+    if shape == "b1":
+        c = build_decode_case([8192], q_len=1, heads=16, topk=2048, seed=401, packed=packed)
+    else:
+        ctx = syn.log_uniform_contexts(64, 4096, 32768, 402)
+        c = build_decode_case(ctx, q_len=1, heads=16, topk=2048, seed=402, packed=packed)
+    c["q"] = (c["q"].float() * 8.0).to(torch.bfloat16)  # N(0, 0.25) * 8 -> std 4
+    out, lse = run_decode(c)
+    ref, ref_lse = oracle_decode(c)
+    # few records dominate each row: the outputs are far from the near-zero
+    # average of a near-uniform softmax over independent rows
+    assert np.abs(ref).mean() > 0.1
+    per_row_check(out, ref, lse, ref_lse)
+
+
+# ---- extreme bitmaps ---------------------------------------------------------------------------
+
+def extreme_rows(rng):
+    """Rows whose top-256 magnitudes fill chosen 64-coordinate groups, with
+    names; large values ~N(0,1)*10, the rest tiny."""
+    rows, names = [], []
+
+    def groups(full, partial=None):
+        x = rng.standard_normal(512).astype(np.float32) * 1e-3
+        for g in full:  # magnitudes 20..30, random signs
+            x[64 * g:64 * g + 64] = ((20 + 10 * rng.random(64)) *
+                                     np.where(rng.random(64) < 0.5, 1, -1)).astype(np.float32)
+        if partial:
+            for g, idx in partial.items():
+                x[64 * g + np.asarray(idx)] = 25.0 + rng.random(len(idx)).astype(np.float32)
+        return x
+
+    for full, name in (((0, 1, 2, 3), "words 0-3 only"), ((4, 5, 6, 7), "words 4-7 only"),
+                       ((0, 2, 4, 6), "even words"), ((1, 3, 5, 7), "odd words, tail full"),
+                       ((7, 0, 1, 2), "tail + 0-2")):
+        rows.append(groups(full))
+        names.append(name)
+    rows.append(groups((0, 1, 2), {3: list(range(63)), 7: [5]}))
+    names.append("word 3 has 63, tail 1")
+    rows.append(groups((), {g: list(range(32)) for g in range(8)}))
+    names.append("half of every word")
+    rows.append(groups((), {g: list(range(0, 64, 2)) for g in range(8)}))
+    names.append("every other coordinate")
+    rows.append(groups((5, 6, 7, 0), {}))
+    names.append("tail + 5, 6, 0")
+    for r, name in ((np.arange(512), "arange"), (-np.arange(512), "-arange"),
+                    (np.zeros(512), "zeros"), (np.ones(512), "ones")):
+        rows.append(r.astype(np.float32))
+        names.append(name)
+    return np.stack(rows), names
+
+
+def test_extreme_bitmaps_pack_reconstruct_and_decode():
+    banner("extreme bitmaps")
+    rng = np.random.default_rng(410)
+    rows, names = extreme_rows(rng)
+    n_ext = rows.shape[0]
+    # 128 records: the extreme rows repeated (with sign flips and scales)
+    reps = [rows * s for s in (1.0, -1.0, 0.25, 3.0, -7.0, 0.5, 2.0, -1.5, 1.25, -0.75)]
+    x = np.concatenate(reps)[:128]
+    x = torch.from_numpy(x)
+    contexts = [128]
+    table = np.array([[1, 0]], np.int32)  # logical record r -> page table[r // 64]
+    slots = (table[0, np.arange(128) // 64] * 64 + np.arange(128) % 64).astype(np.int32)
+    for dtype in (torch.float32, torch.bfloat16):
+        pool = gpu_pack(x.to(dtype), slots, 2)
+        ref_pool = oracle_pack(x.to(dtype), slots, 2)
+        assert_pool_equal(pool, ref_pool)
+        recs = ref_pool.reshape(-1, 328)
+        # the intended structures are present: empty and full bitmap words,
+        # fully pruned groups (scale byte 105)
+        words = recs[slots[:n_ext], 256:320].reshape(n_ext, 8, 8)
+        pops = np.unpackbits(words, axis=2).sum(axis=2)
+        assert (pops == 0).any() and (pops == 64).any()
+        assert (recs[slots[:n_ext], 320:] == 105).any()
+        assert pops[0, :4].sum() == 256 and pops[0, 4:].sum() == 0, names[0]
+        assert pops[1, 4:].sum() == 256 and pops[1, :4].sum() == 0, names[1]
+        # reconstruct every record, with RoPE and without, bit-exact
+        freqs = syn.rope_freqs(4 * 128)
+        phys = slots.reshape(1, -1)
+        raw = np.arange(128, dtype=np.int32).reshape(1, -1)
+        lens = np.array([128], np.int32)
+        out = torch.empty((128, 512), dtype=torch.bfloat16, device=DEV)
+        remnant.unpack_gather_bf16(pool, torch.from_numpy(phys).to(DEV),
+                                   torch.from_numpy(raw).to(DEV), torch.from_numpy(lens).to(DEV),
+                                   freqs.to(DEV), out, fused_rope=True)
+        plain = torch.empty((128, 512), dtype=torch.bfloat16, device=DEV)
+        remnant.unpack_gather_bf16(pool, torch.from_numpy(phys).to(DEV), None,
+                                   torch.from_numpy(lens).to(DEV), None, plain)
+        torch.cuda.synchronize()
+        want = oracle.unpack_gather(ref_pool, phys, raw, lens, torch.view_as_real(freqs).numpy())
+        assert np.array_equal(syn.bf16_bits(out), want)
+        assert np.array_equal(syn.bf16_bits(plain), oracle.unpack_gather(ref_pool, phys, None, lens))
+        # Direct decode over all of them (and over the extreme rows alone), with a
+        # realistic spread and without
+        for q_scale, topk in ((0.5, 128), (6.0, 128), (6.0, n_ext)):
+            g = torch.Generator().manual_seed(411)
+            q = (torch.randn(1, 2, 16, 512, generator=g) * q_scale).to(torch.bfloat16)
+            idx = np.stack([np.random.default_rng(412 + s).permutation(128)[:topk]
+                            if topk == 128 else np.arange(topk) for s in range(2)])
+            idx = idx.astype(np.int32).reshape(1, 2, topk)
+            c = dict(pool=pool, table=table, idx=idx, lens=np.array([topk, topk], np.int32),
+                     q=q, sink=torch.randn(16, generator=g), freqs=freqs, contexts=contexts,
+                     packed=True)
+            out_d, lse_d = run_decode(c)
+            ref, ref_lse = oracle_decode(c)
+            per_row_check(out_d, ref, lse_d, ref_lse)
+
+
+# ---- graph replay with changing inputs --------------------------------------------------------
+
+@pytest.mark.parametrize("batch,heads,topk", [(8, 64, 64), (1, 16, 2048)])
+def test_direct_decode_graph_replay_with_changed_inputs(batch, heads, topk):
+    """The decode (and its split combine) captured once; q, indices, lengths
+    and the records change in place between replays; every replay equals an
+    eager call bit for bit and the oracle within tolerance."""
+    banner(f"decode graph replay B={batch} H={heads} topk={topk}")
+    rng = np.random.default_rng(420 + batch)
+    contexts = [int(v) for v in rng.integers(max(topk, 200), 4 * topk + 300, batch)]
+    c = build_decode_case(contexts, q_len=1, heads=heads, topk=topk, seed=421 + batch)
+    tokens = batch
+    q = c["q"].to(DEV)
+    bt = torch.from_numpy(c["table"]).to(DEV)
+    idx = torch.from_numpy(c["idx"]).to(DEV)
+    lens = torch.from_numpy(c["lens"]).to(DEV)
+    seq = torch.tensor(contexts, dtype=torch.int32, device=DEV)
+    sink = c["sink"].to(DEV)
+    freqs = c["freqs"].to(DEV)
+    _, need = remnant.get_decode_metadata(tokens, heads, topk)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=DEV)
+    out = torch.empty_like(q)
+    lse = torch.empty((batch, 1, heads), dtype=torch.float32, device=DEV)
+    eager_out = torch.empty_like(q)
+    eager_lse = torch.empty_like(lse)
+
+    def call(o, l):
+        remnant.remnant_sparse_decode_fwd(q, c["pool"], bt, idx, seqlens=seq, topk_length=lens,
+                                          sink=sink, freqs_cis=freqs, out=o, lse=l, workspace=ws)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call(out, lse)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call(out, lse)
+    torch.cuda.synchronize()
+    slots_all = []
+    for b, n in enumerate(contexts):
+        r = np.arange(n)
+        slots_all.append(c["table"][b, r // 64] * 64 + r % 64)
+    slots_all = np.concatenate(slots_all).astype(np.int32)
+    for it in range(3):
+        g = torch.Generator().manual_seed(430 + it)
+        q.copy_((torch.randn(q.shape, generator=g) * (0.5 + 2 * it)).to(torch.bfloat16))
+        new_idx, new_lens = syn.topk_indices(contexts, 1, topk, seed=431 + it)
+        new_lens = np.minimum(new_lens, np.array([topk - 7 * it] * batch, np.int32))
+        idx.copy_(torch.from_numpy(new_idx))
+        lens.copy_(torch.from_numpy(new_lens))
+        # re-pack a third of the records with new latents in place
+        pick = np.random.default_rng(432 + it).choice(slots_all.size, slots_all.size // 3,
+                                                      replace=False)
+        x_new = syn.latents(pick.size, seed=433 + it)
+        remnant.pack_rows_fused(x_new.to(DEV), torch.ones(512, device=DEV), 1e-6,
+                                torch.from_numpy(slots_all[pick]).to(DEV), c["pool"])
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        call(eager_out, eager_lse)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager_out.view(torch.int16)), it
+        assert torch.equal(lse, eager_lse), it
+        c["q"] = q.cpu()
+        c["idx"] = new_idx
+        c["lens"] = new_lens
+        ref, ref_lse = oracle_decode(c)
+        per_row_check(out.float().cpu().numpy(), ref, lse.cpu().numpy(), ref_lse)
+
+
+# ---- Native store FP32, batched decode at 4k-128k tokens -----------------------------------
+
+def test_native_store_bit_exact_fp32_input_and_weight():
+    banner("native store fp32")
+    g = torch.Generator().manual_seed(440)
+    n = 768
+    x = torch.randn(n, 512, generator=g) * torch.exp(torch.linspace(-3, 3, 512))
+    x[::37] *= 1e-30
+    x[5::53] = torch.arange(512, dtype=torch.float32) % 5
+    w = np.linspace(0.25, 2.0, 512).astype(np.float32)
+    slots = np.random.default_rng(440).permutation(n).astype(np.int32)
+    slots[::29] = -1
+    positions = np.random.default_rng(441).integers(0, 2000, n).astype(np.int32)
+    positions[3] = 10_000  # beyond the table: skipped
+    freqs = syn.rope_freqs(4 * 2048)
+    pool = remnant.LatentPool(n // 64, fmt="native", device=DEV)
+    pool.buffer.fill_(0x77)
+    remnant.native_store_rows(x.to(DEV), torch.from_numpy(w).to(DEV), 1e-5,
+                              torch.from_numpy(slots).to(DEV), torch.from_numpy(positions).to(DEV),
+                              freqs.to(DEV), pool)
+    torch.cuda.synchronize()
+    ref = np.full((n // 64, oracle.NATIVE_PAGE_BYTES), 0x77, np.uint8)
+    oracle.native_pack_rows_paged(x.numpy(), w, 1e-5, slots, positions,
+                                  torch.view_as_real(freqs).numpy(), ref)
+    assert np.array_equal(pool.layer().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("packed", [True, False], ids=["direct", "native"])
+def test_decode_batch64_contexts_up_to_128k_tokens(packed):
+    """The batched configuration at its full context range: 64 requests of
+    4k-128k tokens (1k-32k records), top-k 2048."""
+    banner(f"decode B=64 4k-128k packed={packed}")
+    ctx = syn.log_uniform_contexts(64, 4096, 131072, 7)
+    assert max(ctx) > 16384
+    c = build_decode_case(ctx, q_len=1, heads=16, topk=2048, seed=450, packed=packed)
+    out, lse = run_decode(c)
+    ref, ref_lse = oracle_decode(c)
+    per_row_check(out, ref, lse, ref_lse)
+
+
+# ---- FP32 pack: full-precision mantissas at the threshold ------------------------------------
+
+def test_pack_fp32_full_precision_threshold_mantissas_and_ties():
+    """About 100k FP32 records never rounded through BF16, nine or so per wave
+    (records 32,768 apart share a wave), each wave's records within 2^+-1 of
+    one scale, so the threshold search starts from the previous record's
+    exponent. Rows get keys that share the threshold's top 16 bits and differ
+    only in mantissa bits 15..0 (the FP32-only histogram levels), and exact
+    FP32 ties at the threshold. Checked byte for byte on 8,000 records."""
+    banner("pack fp32 full-precision threshold")
+    n = 98304 + 4000
+    g = torch.Generator().manual_seed(460)
+    x = torch.randn(n, 512, generator=g, dtype=torch.float32)
+    wave_scale = torch.randint(-20, 21, (32768,), generator=g)
+    k = wave_scale[torch.arange(n) % 32768] + torch.randint(-1, 2, (n,), generator=g)
+    x = x * torch.pow(2.0, k.float())[:, None]
+    xa = x.numpy()
+    rng = np.random.default_rng(461)
+    # threshold neighbourhoods: the 256th largest magnitude t of a row; put 24
+    # keys at t with random low 16 mantissa bits, and 6 exact copies of t
+    t_rows = rng.choice(n, n // 3, replace=False)
+    mags = np.abs(xa[t_rows])
+    t = np.partition(mags, 512 - 256, axis=1)[:, 512 - 256]
+    tb = t.view(np.uint32)
+    for j in range(24):
+        c = rng.integers(0, 512, t_rows.size)
+        low = rng.integers(0, 1 << 16, t_rows.size, dtype=np.uint64).astype(np.uint32)
+        v = ((tb & 0xFFFF0000) | low).view(np.float32)
+        xa[t_rows, c] = np.where(rng.random(t_rows.size) < 0.5, v, -v)
+    for j in range(6):
+        c = rng.integers(0, 512, t_rows.size)
+        xa[t_rows, c] = t * np.where(rng.random(t_rows.size) < 0.5, 1, -1)
+    x = torch.from_numpy(xa)
+    assert (x.view(torch.int32) & 0xFFFF).ne(0).float().mean() > 0.9  # not BF16 values
+    slots = rng.permutation(n).astype(np.int32)
+    pages = n // 64 + 1
+    gpu = gpu_pack(x, slots, pages)
+    pick = np.concatenate([t_rows[:6000], rng.choice(n, 2000, replace=False)])
+    ref = oracle_pack(x[pick], slots[pick], pages)
+    got = gpu.layer().cpu().numpy().reshape(-1, 328)
+    want = ref.reshape(-1, 328)
+    bad = np.nonzero((got[slots[pick]] != want[slots[pick]]).any(axis=1))[0]
+    assert bad.size == 0, f"{bad.size} records differ, first record {int(pick[bad[0]])}"
+
+
+# ---- capacity decode on a pool above 8 GB ---------------------------------------------------
+
+def test_capacity_decode_b128_next_n2_pool_beyond_4gib_offsets():
+    """128 requests x 2 query tokens, top-k 2048 of 32,768-record contexts, on a
+    pool of 450,000 pages (9.4 GB): the requests' pages are scattered over the
+    whole pool, so most records sit past byte offset 2^32. Four requests (eight
+    tokens) are checked against the oracle from a compact copy of their pages;
+    the pack of two requests' records and a reconstruct of high slots are
+    checked byte for byte."""
+    banner("capacity decode B=128 x 2, 9.4 GB pool")
+    batch, q_len, topk, ctx_records = 128, 2, 2048, 32768
+    pool_pages = 450_000
+    contexts = [ctx_records] * batch
+    table, _ = syn.paged_requests(contexts, 470, pool_pages)
+    assert (table.astype(np.int64) * 20992 > (1 << 32)).mean() > 0.4
+    pool = remnant.LatentPool(pool_pages, device=DEV)
+    w = torch.ones(512, device=DEV)
+    tab = torch.from_numpy(table).to(DEV)
+    gc = torch.Generator().manual_seed(470)
+    sigma = torch.exp(torch.empty(512).uniform_(np.log(0.1), np.log(10.0), generator=gc)).to(DEV)
+    r = torch.arange(ctx_records, device=DEV, dtype=torch.int64)
+
+    def request_latents(b):
+        g = torch.Generator(device=DEV).manual_seed(1000 + b)
+        return (torch.randn(ctx_records, 512, device=DEV, generator=g) * sigma).to(torch.bfloat16)
+
+    for b in range(batch):
+        slot = (tab[b, r // 64].to(torch.int64) * 64 + r % 64).to(torch.int32)
+        remnant.pack_rows_fused(request_latents(b), w, 1e-6, slot, pool)
+    idx, lens = syn.topk_indices(contexts, q_len, topk, seed=471)
+    g = torch.Generator().manual_seed(472)
+    q = (torch.randn(batch, q_len, 16, 512, generator=g) * 2.0).to(torch.bfloat16)
+    sink = torch.randn(16, generator=g)
+    freqs = syn.rope_freqs(4 * ctx_records)
+    out, lse = remnant.remnant_sparse_decode_fwd(
+        q.to(DEV), pool, tab, torch.from_numpy(idx).to(DEV),
+        seqlens=torch.tensor(contexts, dtype=torch.int32, device=DEV),
+        topk_length=torch.from_numpy(lens).to(DEV), sink=sink.to(DEV), freqs_cis=freqs.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
+    sample = [0, 41, 90, 127]
+    # compact pool of the sampled requests' pages, table remapped to it
+    pages = torch.from_numpy(table[sample].ravel().astype(np.int64)).to(DEV)
+    compact = pool.layer().index_select(0, pages).cpu().numpy()
+    ctable = np.arange(len(sample) * table.shape[1], dtype=np.int32).reshape(len(sample), -1)
+    sub_lens = lens.reshape(batch, q_len)[sample].ravel()
+    ref, ref_lse = oracle.sparse_decode(
+        syn.bf16_bits(q[sample]).reshape(len(sample), q_len, 16, 512), compact, True, ctable,
+        np.array([ctx_records] * len(sample), np.int32), idx[sample], sub_lens, sink.numpy(),
+        torch.view_as_real(freqs).numpy(), 1 / np.sqrt(512))
+    per_row_check(out[sample].float().cpu().numpy(), ref, lse[sample].cpu().numpy(), ref_lse)
+    # the pack at high offsets: two requests' records against the oracle
+    for b in (41, 127):
+        xs = request_latents(b).float().cpu()
+        rows = np.arange(0, ctx_records, 7)  # a seventh of the records
+        want = oracle_pack(xs[rows], rows.astype(np.int32), ctx_records // 64)
+        i = sample.index(b)
+        got = compact[i * 512:(i + 1) * 512].reshape(-1, 328)[rows]
+        assert np.array_equal(got, want.reshape(-1, 328)[rows]), b
+    # reconstruct from the big pool at the highest slots
+    hi_pages = np.argsort(table[sample].ravel())[-64:]
+    rows = (hi_pages[:, None] * 64 + np.arange(0, 64, 8)[None]).ravel()  # compact rows
+    big = (table[sample].ravel()[hi_pages][:, None].astype(np.int64) * 64 +
+           np.arange(0, 64, 8)[None]).ravel()
+    assert big.max() * 328 > (1 << 32) and big.max() < (1 << 31)
+    out_r = torch.empty((big.size, 512), dtype=torch.bfloat16, device=DEV)
+    remnant.unpack_gather_bf16(pool, torch.from_numpy(big.astype(np.int32)).view(1, -1).to(DEV),
+                               None, torch.tensor([big.size], dtype=torch.int32, device=DEV),
+                               None, out_r)
+    torch.cuda.synchronize()
+    want = oracle.unpack_gather(compact, rows.astype(np.int32).reshape(1, -1), None,
+                                np.array([rows.size], np.int32))
+    assert np.array_equal(syn.bf16_bits(out_r), want)
+    del pool
+    torch.cuda.empty_cache()

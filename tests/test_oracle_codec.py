@@ -437,3 +437,29 @@ def test_adapter_is_lossless_and_encodes_invalid_rows_as_zero_rows():
         if not rows[i].any():
             assert not data.any() and list(scales) == [105] * 7 + [0]
     assert sum(not r.any() for r in rows) > 20
+
+
+def test_array_helpers_match_torch_and_ieee_float32():
+    """The oracle's array forms, used to check the GPU's hardware rounding,
+    agree with library routines: E4M3 encode with torch's float8_e4m3fn cast
+    on every BF16 magnitude <= 448 and both signs; dequantisation with torch's
+    float8 -> float32 cast times 2^(s - 127) rounded by torch's bfloat16 cast
+    for every finite code and scale byte 105..247; the RMS reciprocal with
+    numpy's correctly rounded float32 sqrt and division."""
+    mags = all_bf16_magnitudes(448.0)
+    q = np.concatenate([mags, -mags]).astype(np.float32)
+    want = torch.from_numpy(q).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.e4m3_encode_array(q), want)
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
+    for s in (105, 110, 120, 127, 128, 140, 200, 247):
+        vals = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).float() * 2.0 ** (s - 127)
+        want = vals.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        got = oracle.e4m3_dequant_array(codes, np.full(codes.shape, s, np.uint8))
+        assert np.array_equal(got, want), s
+    rng = np.random.default_rng(9)
+    sumsq = rng.integers(0, 0x7F800000, 200000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    for eps in (0.0, 1e-6):
+        x = sumsq * np.float32(1.0 / 512.0) + np.float32(eps)
+        want = (np.float32(1.0) / np.sqrt(x.astype(np.float32))).astype(np.float32)
+        got = oracle.rms_scale_array(sumsq, np.full(sumsq.shape, eps, np.float32))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
