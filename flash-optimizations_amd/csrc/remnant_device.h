@@ -137,24 +137,23 @@ __device__ __forceinline__ uint32_t fp8_pair_to_bf16(uint32_t codes, float scale
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// RN(1 / RN(sqrt(x))) for x = sumsq / 512 + eps (wave-uniform). For
-// 2^-96 <= x < 2^128 the root s lies in [2^-48, 2^64), where v_sqrt_f32 is
-// the correctly rounded root and one Newton step from v_rcp_f32,
-// fma(fma(-s, r0, 1), r0, r0), equals __fdiv_rn(1, s); other x take the
-// general sequence.
+// RN(1 / RN(sqrt(x))) for x = sumsq / 512 + eps (wave-uniform). The root is
+// the compiler's correctly rounded square root (v_sqrt_f32 alone is not: for
+// x = 1e-6 it returns the lower neighbour of RN(sqrt(x))). For
+// 2^-96 <= x < 2^128 the root s lies in [2^-48, 2^64), where one Newton step
+// from v_rcp_f32, fma(fma(-s, r0, 1), r0, r0), equals the correctly rounded
+// 1 / s; other x take the correctly rounded division.
 __device__ __forceinline__ bool inv_root_fast_range(uint32_t xb) {
   return xb - 0x0f800000u < 0x7f800000u - 0x0f800000u;
 }
-__device__ __forceinline__ float inv_root_fast(float x) {
-  const float s = __builtin_amdgcn_sqrtf(x);
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+__device__ __forceinline__ float recip_newton(float s) {
   const float r0 = __builtin_amdgcn_rcpf(s);
   return __builtin_fmaf(__builtin_fmaf(-s, r0, 1.0f), r0, r0);
 }
-__device__ __forceinline__ float inv_root_general(float x) {
-  return __fdiv_rn(1.0f, __fsqrt_rn(x));
-}
 __device__ __forceinline__ float inv_root(float x) {
-  return inv_root_fast_range(__float_as_uint(x)) ? inv_root_fast(x) : inv_root_general(x);
+  const float s = sqrt_rn(x);
+  return inv_root_fast_range(__float_as_uint(x)) ? recip_newton(s) : 1.0f / s;
 }
 __device__ __forceinline__ float inv_rms(float sumsq, float eps) {
   const float x = sumsq * (1.0f / 512.0f) + eps;

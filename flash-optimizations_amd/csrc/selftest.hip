@@ -80,8 +80,16 @@ __global__ __launch_bounds__(kThreads) void fp8_decode_kernel(uint16_t* out) {
   out[i] = r;
 }
 
-// Fast reciprocal root vs the correctly rounded sequence over FP32 bit
-// patterns [first, end) inside its range.
+// Neighbouring floats of a positive finite v.
+__device__ __forceinline__ double below(float v) { return (double)u2f(f2u(v) - 1); }
+__device__ __forceinline__ double above(float v) { return (double)u2f(f2u(v) + 1); }
+
+// Correct rounding of the store's root and reciprocal, proved exactly for FP32
+// bit patterns [first, end) (positive finite x): s = RN(sqrt(x)) iff x lies
+// strictly between the squares of the midpoints around s, and r = RN(1 / s)
+// iff 1 lies strictly between s times the midpoints around r. Midpoints of
+// adjacent floats have 25 significant bits, so the midpoints and these
+// products are exact in double precision, and no tie can occur.
 __global__ __launch_bounds__(kThreads) void inv_root_kernel(uint32_t first, uint32_t end,
                                                             unsigned long long* result) {
   unsigned long long bad = 0;
@@ -89,9 +97,14 @@ __global__ __launch_bounds__(kThreads) void inv_root_kernel(uint32_t first, uint
   for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; first + i < end;
        i += (uint64_t)gridDim.x * kThreads) {
     const uint32_t xb = first + (uint32_t)i;
-    if (!inv_root_fast_range(xb)) continue;
     const float x = u2f(xb);
-    if (__float_as_uint(inv_root_fast(x)) != __float_as_uint(inv_root_general(x))) {
+    const float s = sqrt_rn(x);
+    const float r = inv_root(x);
+    const double ds = s, dr = r, dx = x;
+    const double slo = 0.5 * (ds + below(s)), shi = 0.5 * (ds + above(s));
+    const double rlo = 0.5 * (dr + below(r)), rhi = 0.5 * (dr + above(r));
+    const bool ok = slo * slo < dx && dx < shi * shi && rlo * ds < 1.0 && 1.0 < rhi * ds;
+    if (!ok) {
       ++bad;
       first_bad = first_bad < xb ? first_bad : xb;
     }

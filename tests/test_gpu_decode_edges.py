@@ -37,11 +37,16 @@ def banner(msg):
 
 
 def per_row_check(out, ref, lse=None, ref_lse=None):
-    """Tolerance per (token, head) row of [.., 512] outputs."""
+    """Tolerance per (token, head) row of [.., 512] outputs: the reference's
+    attention bar elementwise, |out - ref| <= 0.02 + 0.02 |ref| (output and LSE,
+    atol = rtol = 0.02, docs/report.md:20), and cosine >= 0.9999 for every row.
+    (A pure max-abs of 0.02 cannot hold for BF16 outputs beyond |8|, where half
+    a BF16 ulp is 0.031.)"""
     o = out.reshape(-1, 512).astype(np.float64)
     r = ref.reshape(-1, 512).astype(np.float64)
+    excess = (np.abs(o - r) - (OUT_TOL + OUT_TOL * np.abs(r))).max(axis=1)
+    assert excess.max() <= 0, f"row {int(excess.argmax())}: beyond atol + rtol by {excess.max()}"
     err = np.abs(o - r).max(axis=1)
-    assert err.max() <= OUT_TOL, f"row {int(err.argmax())}: max-abs {err.max()}"
     no, nr = np.linalg.norm(o, axis=1), np.linalg.norm(r, axis=1)
     live = (no > 0) | (nr > 0)
     cos = (o * r).sum(axis=1)[live] / np.maximum(no * nr, 1e-300)[live]
@@ -49,7 +54,8 @@ def per_row_check(out, ref, lse=None, ref_lse=None):
     if lse is not None:
         finite = np.isfinite(ref_lse)
         assert np.array_equal(finite, np.isfinite(lse))
-        assert np.abs(lse[finite] - ref_lse[finite]).max() <= OUT_TOL
+        assert (np.abs(lse[finite] - ref_lse[finite]) <=
+                OUT_TOL + OUT_TOL * np.abs(ref_lse[finite])).all()
     return float(err.max()), float(cos.min())
 
 
