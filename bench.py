@@ -102,6 +102,9 @@ def bulk(torch, remnant, args):
     def pack():
         remnant.pack_rows_fused(x, w, 1e-6, slots, pool)
 
+    def pack_fp32():
+        remnant.pack_rows_fused(x32, w, 1e-6, slots, pool)
+
     def recon():
         remnant.unpack_gather_bf16(pool, physical, None, lengths, None, out)
 
@@ -144,8 +147,20 @@ def bulk(torch, remnant, args):
     e2[1].record()
     torch.cuda.synchronize()
     rope_ms = e2[0].elapsed_time(e2[1]) / k
+    # the pack on FP32 input (the production producer's dtype), separately
+    x32 = x.float()
+    for _ in range(2):
+        pack_fp32()
+    e3 = events(torch, 2)
+    e3[0].record()
+    for _ in range(k):
+        pack_fp32()
+    e3[1].record()
+    torch.cuda.synchronize()
+    pack32_ms = e3[0].elapsed_time(e3[1]) / k
+    del x32
     return dict(n=n, steps=k, total_ms=total_ms, wall_ms=wall, pack_ms=pack_ms,
-                recon_ms=recon_ms, rope_ms=rope_ms, warmup_run=done)
+                recon_ms=recon_ms, rope_ms=rope_ms, pack32_ms=pack32_ms, warmup_run=done)
 
 
 def build_decode(torch, remnant, contexts, q_len, topk, packed, seed, pool_pages=None, heads=16,
@@ -250,28 +265,38 @@ def decode_leg(torch, remnant, args):
     if not args.no_capacity:
         free, total = torch.cuda.mem_get_info()
         res["hbm_total_bytes"] = total
-        cap_pages = int(0.6 * free) // remnant.config.NATIVE_PAGE_BYTES
-        cases.append(("b128_sq2_h16_topk2048_ctx128k", [32768] * 128, 2,
-                      {"pool_pages": cap_pages}))
+        cases.append(("b128_sq2_h16_topk2048_ctx128k", [32768] * 128, 2, {"fill_hbm": True}))
     for name, contexts, q_len, extra in cases:
         entry = {"batch": len(contexts), "q_len": q_len, "heads": 16, "topk": 2048,
                  "context_records_mean": float(sum(contexts) / len(contexts))}
         for packed in (True, False):
             log(f"decode {name} packed={packed}")
-            c = build_decode(torch, remnant, contexts, q_len, 2048, packed, 11,
-                             extra.get("pool_pages"))
+            pool_pages = None
+            if extra.get("fill_hbm"):
+                # the capacity case: a pool of this format filling the free HBM
+                # (less 8 GB for the decode's own tensors)
+                torch.cuda.empty_cache()
+                free, _ = torch.cuda.mem_get_info()
+                page = (remnant.config.PACKED_PAGE_BYTES if packed
+                        else remnant.config.NATIVE_PAGE_BYTES)
+                pool_pages = (free - (8 << 30)) // page
+            c = build_decode(torch, remnant, contexts, q_len, 2048, packed, 11, pool_pages)
             us, _, _ = time_decode(torch, remnant, c)
             key = "direct_packed" if packed else "native"
             byt = decode_bytes(c, rope_table=False)
             entry[key] = {"us_per_step": us, "tokens_per_s": c["q"].shape[0] * q_len / (us * 1e-6),
                           "algorithmic_bytes": byt, "GBps": byt / (us * 1e3),
                           "hbm_frac": byt / (us * 1e3) / HBM_PEAK_GBS,
-                          "pool_bytes": c["pool"].nbytes()}
+                          "pool_bytes": c["pool"].nbytes(),
+                          "records_resident": c["pool"].rows}
             if packed:
                 entry[key]["algorithmic_bytes_with_rope_table"] = decode_bytes(c, True)
             del c
             torch.cuda.empty_cache()
         entry["packed_over_native_time"] = entry["direct_packed"]["us_per_step"] / entry["native"]["us_per_step"]
+        if extra.get("fill_hbm"):
+            entry["records_resident_packed_over_native"] = (
+                entry["direct_packed"]["records_resident"] / entry["native"]["records_resident"])
         res[name] = entry
     if not args.no_reference_shapes:
         res["reference_shapes"] = reference_shapes_leg(torch, remnant)
@@ -410,25 +435,69 @@ def host_cache_leg(torch, remnant):
     return res
 
 
-def cpu_leg(args):
-    """Oracle (plain C, one thread) on a bounded sample of the bulk workload."""
+def cpu_leg(args, torch, remnant):
+    """The CPU path: the oracle (plain C, a port of the reference's
+    pack/reconstruct and gather-softmax-sink decode) timed on this host on
+    bounded samples of the same workloads, on one thread and on every core of
+    the host's share: pack + reconstruct of ``cpu_sample`` records of the bulk
+    workload's distribution (random slots), and the decode at the batch-1 and
+    batch-64 shapes of the decode leg (16 heads, top-k 2048; the same pools,
+    built on the GPU outside the timed region; the oracle computes in double
+    precision)."""
     import numpy as np
 
     import oracle
+    host = os.cpu_count() or 1
+    threads_all = max(1, min(host, int(os.environ.get("OMP_NUM_THREADS", "0") or host)))
     n = args.cpu_sample
     x = oracle.synthetic_latents(n)
     slots = np.random.default_rng(1).permutation(n).astype(np.int32)
     k = args.keep_count
-    pool = np.zeros(((n + 63) // 64, oracle.page_bytes(k)), np.uint8)
-    t0 = time.perf_counter()
-    oracle.pack_rows_paged(x, np.ones(512, np.float32), 1e-6, slots, pool, k)
-    t1 = time.perf_counter()
-    oracle.unpack_gather(pool, slots[None], None, np.array([n], np.int32), keep_count=k)
-    t2 = time.perf_counter()
-    return {"value": n / (t2 - t0), "unit": "records/s", "cores": 1, "kind": "port",
-            "sample": f"{n} of the 1,048,576-record pack + reconstruct workload, one thread "
-                      f"(pack {n / (t1 - t0):.0f} rec/s, reconstruct {n / (t2 - t1):.0f} rec/s)",
-            "host_cpus": os.cpu_count()}
+    pr = {}
+    for threads in sorted({1, threads_all}):
+        oracle.set_threads(threads)
+        pool = np.zeros(((n + 63) // 64, oracle.page_bytes(k)), np.uint8)
+        t0 = time.perf_counter()
+        oracle.pack_rows_paged(x, np.ones(512, np.float32), 1e-6, slots, pool, k)
+        t1 = time.perf_counter()
+        oracle.unpack_gather(pool, slots[None], None, np.array([n], np.int32), keep_count=k)
+        t2 = time.perf_counter()
+        pr[threads] = {"records_per_s": n / (t2 - t0), "pack_records_per_s": n / (t1 - t0),
+                       "reconstruct_records_per_s": n / (t2 - t1)}
+    syn = remnant.synthetic
+    dec = {}
+    for name, contexts in (("b1_h16_topk2048_ctx8192", [8192]),
+                           ("b64_h16_topk2048_ctx4k_128k",
+                            syn.log_uniform_contexts(64, 4096, 131072, 7))):
+        c = build_decode(torch, remnant, contexts, 1, 2048, True, 11)
+        pool = c["pool"].layer().cpu().numpy()
+        q = syn.bf16_bits(c["q"]).reshape(c["q"].shape)
+        table = c["table"].cpu().numpy()
+        idx, lens = c["idx"].cpu().numpy(), c["lens"].cpu().numpy()
+        seq = np.array(contexts, np.int32)
+        sink = c["sink"].cpu().numpy()
+        freqs = torch.view_as_real(c["freqs"].cpu()).numpy()
+        del c
+        torch.cuda.empty_cache()
+        entry = {"batch": len(contexts), "tokens": len(contexts)}
+        for threads in sorted({1, threads_all}):
+            oracle.set_threads(threads)
+            t0 = time.perf_counter()
+            oracle.sparse_decode(q, pool, True, table, seq, idx, lens, sink, freqs,
+                                 1 / math.sqrt(512))
+            dt = time.perf_counter() - t0
+            entry[f"threads_{threads}"] = {"us_per_step": dt * 1e6,
+                                           "tokens_per_s": len(contexts) / dt}
+        dec[name] = entry
+    oracle.set_threads(1)
+    best = pr[threads_all]
+    return {"value": best["records_per_s"], "unit": "records/s", "cores": threads_all,
+            "kind": "port",
+            "sample": f"{n} of the 1,048,576-record pack + reconstruct workload on "
+                      f"{threads_all} threads (one thread: {pr[1]['records_per_s']:.0f} "
+                      f"records/s); decode at batch 1 and 64 in `decode`",
+            "pack_reconstruct": {f"threads_{t}": v for t, v in pr.items()},
+            "decode": dec, "host_cpus": host}
 
 
 def load_traffic():
@@ -473,6 +542,8 @@ def main():
                         "GBps": n * recon_bytes / (recon_ms * 1e6)},
         "reconstruct_rope_table": {"ms": b["rope_ms"], "records_per_s": n / (b["rope_ms"] * 1e-3),
                                    "GBps": n * (RECON_ROPE_BYTES + extra) / (b["rope_ms"] * 1e6)},
+        "pack_fp32_input": {"ms": b["pack32_ms"], "records_per_s": n / (b["pack32_ms"] * 1e-3),
+                            "GBps": n * (pack_bytes + 1024) / (b["pack32_ms"] * 1e6)},
     }
     dominant = "pack" if pack_ms >= recon_ms else "reconstruct"
     dom_ms = pack_ms if dominant == "pack" else recon_ms
@@ -500,6 +571,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
+        "input_dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "bulk pack + reconstruct of 1,048,576 C4 records (BF16 "
                                "512-coordinate latents, N(0,1) x log-uniform[0.1,10] per-coordinate "
@@ -521,8 +593,8 @@ def main():
         log("host cache transfers")
         line["host_cache"] = host_cache_leg(torch, remnant)
     if not (args.quick or args.no_cpu):
-        log("cpu baseline (oracle, one thread)")
-        line["cpu_baseline"] = cpu_leg(args)
+        log("cpu baseline (oracle, one thread and all cores)")
+        line["cpu_baseline"] = cpu_leg(args, torch, remnant)
     print(json.dumps(line), flush=True)
 
 

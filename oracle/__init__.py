@@ -79,6 +79,8 @@ def lib():
         _lib.orc_unpack_gather_k.argtypes = [vp, i64, ctypes.c_int, vp, i64, i64, vp, i64,
                                              i64, vp, i64, i64, i64, vp, i64, vp]
         _lib.orc_normalize.argtypes = [vp, vp, vp, f32, vp]
+        _lib.orc_set_threads.argtypes = [ctypes.c_int]
+        _lib.orc_get_threads.restype = ctypes.c_int
         _lib.orc_e4m3_encode_n.argtypes = [vp, i64, vp]
         _lib.orc_e4m3_dequant_n.argtypes = [vp, vp, i64, vp]
         _lib.orc_rms_scale_n.argtypes = [vp, vp, i64, vp]
@@ -103,6 +105,16 @@ def lib():
                                                i64, i64, vp, vp, i64, vp, vp, i64, vp, i64, vp,
                                                vp, vp, i64, f32, vp, vp]
     return _lib
+
+
+def set_threads(n: int) -> None:
+    """Threads of the batch loops (pack, reconstruct, decode); results do not
+    depend on it. With more than one thread pack slots must be distinct."""
+    lib().orc_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().orc_get_threads())
 
 
 def _p(a: np.ndarray | None):

@@ -60,6 +60,12 @@
 #define NATIVE_DATA_BYTES 576 /* 448 e4m3 + 64 bf16 */
 #define NATIVE_PAGE_BYTES (PAGE_RECORDS * (NATIVE_DATA_BYTES + SCALE_BYTES))
 
+/* Threads of the batch loops below (records, rows and tokens are
+ * independent; every result is computed the same way on any thread count). */
+static int g_threads = 1;
+void orc_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+int orc_get_threads(void) { return g_threads; }
+
 static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 
@@ -251,11 +257,13 @@ static inline int64_t page_of(int64_t slot) { return slot / PAGE_RECORDS; }
 static inline int64_t record_bytes_k(int K) { return K + BITMAP_BYTES + SCALE_BYTES; }
 static inline int64_t page_bytes_k(int K) { return PAGE_RECORDS * record_bytes_k(K); }
 
-/* Pack rows into the paged pool at dst_slot[i] (negative slots are skipped). */
+/* Pack rows into the paged pool at dst_slot[i] (negative slots are skipped).
+ * With more than one thread the slots must be distinct. */
 void orc_pack_rows_paged_k(const float* x, const float* w, float eps, int K,
                            const int32_t* slot, int64_t rows, uint8_t* pool,
                            int64_t pool_pages) {
     const int64_t rb = record_bytes_k(K), pb = page_bytes_k(K);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t i = 0; i < rows; ++i) {
         int64_t s = slot[i];
         if (s < 0 || s >= pool_pages * PAGE_RECORDS) continue;
@@ -311,18 +319,19 @@ void orc_unpack_gather_k(const uint8_t* pool, int64_t pool_pages, int K,
                          const float* freqs, int64_t freq_rows, uint16_t* out) {
     int64_t rows = pool_pages * PAGE_RECORDS;
     const int64_t rb = record_bytes_k(K), pb = page_bytes_k(K);
-    for (int64_t q = 0; q < nq; ++q)
-        for (int64_t k = 0; k < nk; ++k) {
-            uint16_t* o = out + (q * nk + k) * HEAD_DIM;
-            int64_t p = physical[q * ps_q + k * ps_k];
-            int64_t r = raw ? raw[q * rs_q + k * rs_k] : 0;
-            int valid = k < lengths[q * ls] && p >= 0 && p < rows;
-            if (freqs) valid = valid && r >= 0 && r * 4 < freq_rows;
-            if (!valid) { memset(o, 0, HEAD_DIM * 2); continue; }
-            const uint8_t* rec = pool + page_of(p) * pb + (p % PAGE_RECORDS) * rb;
-            orc_unpack_row_k(rec, rec + K + BITMAP_BYTES, K, o);
-            if (freqs) orc_rope_tail(o, freqs + r * 4 * ROPE_PAIRS * 2);
-        }
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t qk = 0; qk < nq * nk; ++qk) {
+        const int64_t q = qk / nk, k = qk % nk;
+        uint16_t* o = out + (q * nk + k) * HEAD_DIM;
+        int64_t p = physical[q * ps_q + k * ps_k];
+        int64_t r = raw ? raw[q * rs_q + k * rs_k] : 0;
+        int valid = k < lengths[q * ls] && p >= 0 && p < rows;
+        if (freqs) valid = valid && r >= 0 && r * 4 < freq_rows;
+        if (!valid) { memset(o, 0, HEAD_DIM * 2); continue; }
+        const uint8_t* rec = pool + page_of(p) * pb + (p % PAGE_RECORDS) * rb;
+        orc_unpack_row_k(rec, rec + K + BITMAP_BYTES, K, o);
+        if (freqs) orc_rope_tail(o, freqs + r * 4 * ROPE_PAIRS * 2);
+    }
 }
 
 void orc_unpack_gather(const uint8_t* pool, int64_t pool_pages, const int32_t* physical,
@@ -468,11 +477,13 @@ void orc_sparse_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t 
                        const int32_t* seqlens, const int32_t* indices, int64_t topk,
                        const int32_t* topk_length, const float* sink, const float* freqs,
                        int64_t freq_rows, float scale, double* out, double* lse) {
-    uint16_t* rows = (uint16_t*)malloc(sizeof(uint16_t) * HEAD_DIM * (topk > 0 ? topk : 1));
-    uint8_t* valid = (uint8_t*)malloc(topk > 0 ? topk : 1);
-    for (int64_t b = 0; b < batch; ++b)
-        for (int64_t s = 0; s < q_len; ++s) {
-            int64_t t = b * q_len + s;
+#pragma omp parallel num_threads(g_threads)
+    {
+        uint16_t* rows = (uint16_t*)malloc(sizeof(uint16_t) * HEAD_DIM * (topk > 0 ? topk : 1));
+        uint8_t* valid = (uint8_t*)malloc(topk > 0 ? topk : 1);
+#pragma omp for schedule(dynamic)
+        for (int64_t t = 0; t < batch * q_len; ++t) {
+            const int64_t b = t / q_len;
             int64_t len = topk_length ? topk_length[t] : topk;
             orc_decode_gather(pool, pool_pages, packed, block_table + b * bt_stride, 1,
                               max_blocks, seqlens ? seqlens[b] : INT64_MAX,
@@ -480,8 +491,9 @@ void orc_sparse_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t 
             orc_sink_attention(q + t * heads * HEAD_DIM, heads, rows, valid, topk, sink,
                                scale, out + t * heads * HEAD_DIM, lse + t * heads);
         }
-    free(rows);
-    free(valid);
+        free(rows);
+        free(valid);
+    }
 }
 
 /* SWA rows of one token: the rows lie in a Native pool (64-record pages) at

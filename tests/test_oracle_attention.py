@@ -167,3 +167,34 @@ def test_joint_swa_decode_matches_reference_formula():
                                             None, sink, freqs, scale)
     np.testing.assert_array_equal(none, plain)
     np.testing.assert_array_equal(none_lse, plain_lse)
+
+
+def test_threaded_batch_loops_give_identical_results():
+    """The CPU baseline runs the oracle's pack, reconstruct and decode loops on
+    every host core; each record, row and token is computed the same way on
+    any thread count."""
+    from remnant import synthetic as syn
+    x = syn.latents(640, seed=90).float().numpy()
+    slots = np.random.default_rng(90).permutation(640).astype(np.int32)
+    q = syn.bf16_bits(syn.latents(3 * 16, seed=91)).reshape(3, 1, 16, 512)
+    table = np.arange(10, dtype=np.int32).reshape(1, 10).repeat(3, 0)
+    idx = np.random.default_rng(92).integers(-1, 640, (3, 1, 300)).astype(np.int32)
+    lens = np.array([300, 17, 0], np.int32)
+    freqs = torch.view_as_real(syn.rope_freqs(4 * 640)).numpy()
+    results = []
+    try:
+        for threads in (1, 4):
+            oracle.set_threads(threads)
+            assert oracle.get_threads() == threads
+            pool = np.zeros((10, oracle.PAGE_BYTES), np.uint8)
+            oracle.pack_rows_paged(x, np.ones(512, np.float32), 1e-6, slots, pool)
+            rows = oracle.unpack_gather(pool, slots.reshape(4, 160), slots.reshape(4, 160),
+                                        np.array([160, 3, 160, 0], np.int32), freqs)
+            out, lse = oracle.sparse_decode(q, pool, True, table, np.full(3, 640, np.int32), idx,
+                                            lens, np.zeros(16, np.float32), freqs,
+                                            1 / np.sqrt(512))
+            results.append((pool, rows, out, lse))
+    finally:
+        oracle.set_threads(1)
+    for a, b in zip(*results):
+        assert np.array_equal(a, b)
