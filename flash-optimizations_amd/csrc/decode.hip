@@ -38,6 +38,7 @@
 // A Native record stages its 576-byte data row (36 pieces) and its scale row.
 // A split count > 1 writes (O/l, m + log2 l) partials merged with the sink by a
 // combine kernel; a single split finalises in place.
+#include <mutex>
 #include <type_traits>
 
 #include "remnant_device.h"
@@ -1097,6 +1098,63 @@ extern "C" int rm_remnant_sparse_decode_fwd(
                              block_table_stride, max_blocks, seqlens, indices, topk, topk_length,
                              Swa(), sink, freqs, freq_rows, softmax_scale, out, lse, workspace,
                              workspace_bytes, stream);
+}
+
+namespace {
+
+// ---- allocation-free variant ----
+// The split partials of rm_remnant_sparse_decode_swa_noalloc_fwd live in this
+// file-scope device array instead of a caller workspace. Each GPU the library
+// runs on holds its own copy until the process ends. In host code `scratch`
+// names a host-side stand-in, never the device array: its device address is
+// looked up once per device (hipGetSymbolAddress, with that device current) and
+// only that address reaches kernels. Every split writes its whole partial slot
+// before the combine reads it, so nothing needs clearing between calls; calls
+// that overlap on one GPU share the array and race.
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (nullptr on failure).
+void* scratch_address() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int rm_remnant_sparse_decode_swa_noalloc_fwd(
+    const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads, const uint8_t* pool,
+    int64_t pool_pages, const int32_t* block_table, int64_t block_table_stride,
+    int64_t max_blocks, const int32_t* seqlens, const int32_t* indices, int64_t topk,
+    const int32_t* topk_length, const uint8_t* swa_pool, int64_t swa_pool_pages,
+    const int32_t* swa_indices, int64_t swa_topk, const int32_t* swa_length, const float* sink,
+    const float* freqs, int64_t freq_rows, float softmax_scale, uint16_t* out, float* lse,
+    void* stream) {
+  // a partial slot set beyond the array is refused before any launch
+  int32_t splits = 0;
+  size_t need = 0;
+  const int st = rm_sparse_decode_workspace_swa(batch * q_len, heads, topk, swa_topk, &splits,
+                                                &need);
+  if (st != RM_OK) return st;
+  if (need > kScratchBytes) return RM_ERR_WORKSPACE;
+  void* ws = nullptr;
+  if (need > 0 && !(ws = scratch_address())) return RM_ERR_LAUNCH;
+  return rm_remnant_sparse_decode_swa_fwd(q, batch, q_len, heads, pool, pool_pages, block_table,
+                                          block_table_stride, max_blocks, seqlens, indices, topk,
+                                          topk_length, swa_pool, swa_pool_pages, swa_indices,
+                                          swa_topk, swa_length, sink, freqs, freq_rows,
+                                          softmax_scale, out, lse, ws, need, stream);
 }
 
 extern "C" int rm_remnant_sparse_decode_swa_fwd(

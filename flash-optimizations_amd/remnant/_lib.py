@@ -66,6 +66,10 @@ SIGNATURES = {
                                                 _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64,
                                                 _vp, _vp, _vp, _i64, _f32, _vp, _vp, _vp, _sz,
                                                 _vp]),
+    "rm_remnant_sparse_decode_swa_noalloc_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp,
+                                                        _i64, _i64, _vp, _vp, _i64, _vp, _vp,
+                                                        _i64, _vp, _i64, _vp, _vp, _vp, _i64,
+                                                        _f32, _vp, _vp, _vp]),
     "rm_native_sparse_decode_swa_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
                                                _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64,
                                                _vp, _vp, _f32, _vp, _vp, _vp, _sz, _vp]),

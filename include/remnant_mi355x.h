@@ -256,6 +256,23 @@ int rm_remnant_sparse_decode_planes_fwd(
     int64_t freq_rows, float softmax_scale, uint16_t* out, float* lse, void* workspace,
     size_t workspace_bytes, void* stream);
 
+/* rm_remnant_sparse_decode_swa_fwd without a workspace argument: the split
+ * partials live in a 32 MiB device array inside the library (one per GPU,
+ * held until the process ends), so the call allocates nothing. No counterpart
+ * in the reference: for callers that cannot allocate (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). A call whose split
+ * plan needs more than 32 MiB (rm_sparse_decode_workspace_swa) returns
+ * RM_ERR_WORKSPACE without launching. Calls that overlap on one GPU share the
+ * array and race; calls on one stream do not. */
+int rm_remnant_sparse_decode_swa_noalloc_fwd(
+    const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads, const uint8_t* pool,
+    int64_t pool_pages, const int32_t* block_table, int64_t block_table_stride,
+    int64_t max_blocks, const int32_t* seqlens, const int32_t* indices, int64_t topk,
+    const int32_t* topk_length, const uint8_t* swa_pool, int64_t swa_pool_pages,
+    const int32_t* swa_indices, int64_t swa_topk, const int32_t* swa_length, const float* sink,
+    const float* freqs, int64_t freq_rows, float softmax_scale, uint16_t* out, float* lse,
+    void* stream);
+
 /* Native control decode: same contract on 584-byte records (tail already rotated). */
 int rm_native_sparse_decode_fwd(const uint16_t* q, int64_t batch, int64_t q_len,
                                 int64_t heads, const uint8_t* pool, int64_t pool_pages,
