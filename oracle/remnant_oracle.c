@@ -437,36 +437,41 @@ void orc_decode_gather(const uint8_t* pool, int64_t pool_pages, int packed,
  * logits l_j = (q_h . K_j) * scale over valid rows; Z = sum exp(l_j) + exp(sink_h);
  * out_h = sum_j exp(l_j) K_j / Z; lse_h = log Z (sink == NULL: no sink term).
  * With no valid row and no sink, out = 0 and lse = -inf. V = K (same row). */
+/* One head of orc_sink_attention (logit: nk doubles of scratch). */
+static void sink_attention_head(const uint16_t* qh, const uint16_t* rows, const uint8_t* valid,
+                                int64_t nk, const float* sink_h, float scale, double* logit,
+                                double* oh, double* lse_h) {
+    double mx = sink_h ? (double)*sink_h : -INFINITY;
+    for (int64_t k = 0; k < nk; ++k) {
+        if (!valid[k]) continue;
+        double acc = 0.0;
+        const uint16_t* kr = rows + k * HEAD_DIM;
+        for (int c = 0; c < HEAD_DIM; ++c)
+            acc += (double)orc_bf16_to_f32(qh[c]) * (double)orc_bf16_to_f32(kr[c]);
+        logit[k] = acc * (double)scale;
+        if (logit[k] > mx) mx = logit[k];
+    }
+    for (int c = 0; c < HEAD_DIM; ++c) oh[c] = 0.0;
+    if (mx == -INFINITY) { *lse_h = -INFINITY; return; }
+    double z = sink_h ? exp((double)*sink_h - mx) : 0.0;
+    for (int64_t k = 0; k < nk; ++k) {
+        if (!valid[k]) continue;
+        double p = exp(logit[k] - mx);
+        z += p;
+        const uint16_t* kr = rows + k * HEAD_DIM;
+        for (int c = 0; c < HEAD_DIM; ++c) oh[c] += p * (double)orc_bf16_to_f32(kr[c]);
+    }
+    for (int c = 0; c < HEAD_DIM; ++c) oh[c] /= z;
+    *lse_h = mx + log(z);
+}
+
 void orc_sink_attention(const uint16_t* q, int64_t heads, const uint16_t* rows,
                         const uint8_t* valid, int64_t nk, const float* sink, float scale,
                         double* out, double* lse) {
     double* logit = (double*)malloc(sizeof(double) * (nk > 0 ? nk : 1));
-    for (int64_t h = 0; h < heads; ++h) {
-        const uint16_t* qh = q + h * HEAD_DIM;
-        double mx = sink ? (double)sink[h] : -INFINITY;
-        for (int64_t k = 0; k < nk; ++k) {
-            if (!valid[k]) continue;
-            double acc = 0.0;
-            const uint16_t* kr = rows + k * HEAD_DIM;
-            for (int c = 0; c < HEAD_DIM; ++c)
-                acc += (double)orc_bf16_to_f32(qh[c]) * (double)orc_bf16_to_f32(kr[c]);
-            logit[k] = acc * (double)scale;
-            if (logit[k] > mx) mx = logit[k];
-        }
-        double* oh = out + h * HEAD_DIM;
-        for (int c = 0; c < HEAD_DIM; ++c) oh[c] = 0.0;
-        if (mx == -INFINITY) { lse[h] = -INFINITY; continue; }
-        double z = sink ? exp((double)sink[h] - mx) : 0.0;
-        for (int64_t k = 0; k < nk; ++k) {
-            if (!valid[k]) continue;
-            double p = exp(logit[k] - mx);
-            z += p;
-            const uint16_t* kr = rows + k * HEAD_DIM;
-            for (int c = 0; c < HEAD_DIM; ++c) oh[c] += p * (double)orc_bf16_to_f32(kr[c]);
-        }
-        for (int c = 0; c < HEAD_DIM; ++c) oh[c] /= z;
-        lse[h] = mx + log(z);
-    }
+    for (int64_t h = 0; h < heads; ++h)
+        sink_attention_head(q + h * HEAD_DIM, rows, valid, nk, sink ? sink + h : NULL, scale,
+                            logit, out + h * HEAD_DIM, lse + h);
     free(logit);
 }
 
@@ -477,6 +482,40 @@ void orc_sparse_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t 
                        const int32_t* seqlens, const int32_t* indices, int64_t topk,
                        const int32_t* topk_length, const float* sink, const float* freqs,
                        int64_t freq_rows, float scale, double* out, double* lse) {
+    const int64_t tokens = batch * q_len;
+    if (tokens < g_threads) {
+        /* few tokens (batch 1): per token, the gather in record chunks and the
+         * heads on all threads -- the same arithmetic per head as below */
+        const int64_t nk = topk > 0 ? topk : 1;
+        uint16_t* rows = (uint16_t*)malloc(sizeof(uint16_t) * HEAD_DIM * nk);
+        uint8_t* valid = (uint8_t*)malloc(nk);
+        for (int64_t t = 0; t < tokens; ++t) {
+            const int64_t b = t / q_len;
+            const int64_t len = topk_length ? topk_length[t] : topk;
+            const int64_t chunk = 64, chunks = (topk + chunk - 1) / chunk;
+#pragma omp parallel for num_threads(g_threads) schedule(dynamic)
+            for (int64_t c = 0; c < chunks; ++c) {
+                const int64_t k0 = c * chunk, k1 = k0 + chunk < topk ? k0 + chunk : topk;
+                orc_decode_gather(pool, pool_pages, packed, block_table + b * bt_stride, 1,
+                                  max_blocks, seqlens ? seqlens[b] : INT64_MAX,
+                                  indices + t * topk + k0, k1 - k0, len - k0, freqs, freq_rows,
+                                  rows + k0 * HEAD_DIM, valid + k0);
+            }
+#pragma omp parallel num_threads(g_threads)
+            {
+                double* logit = (double*)malloc(sizeof(double) * nk);
+#pragma omp for schedule(dynamic)
+                for (int64_t h = 0; h < heads; ++h)
+                    sink_attention_head(q + (t * heads + h) * HEAD_DIM, rows, valid, topk,
+                                        sink ? sink + h : NULL, scale, logit,
+                                        out + (t * heads + h) * HEAD_DIM, lse + t * heads + h);
+                free(logit);
+            }
+        }
+        free(rows);
+        free(valid);
+        return;
+    }
 #pragma omp parallel num_threads(g_threads)
     {
         uint16_t* rows = (uint16_t*)malloc(sizeof(uint16_t) * HEAD_DIM * (topk > 0 ? topk : 1));
