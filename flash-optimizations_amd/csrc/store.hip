@@ -350,6 +350,26 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
   return keep;
 }
 
+// Rows rec, rec + step, ... below end of this wave. Runs: the n rows cut into
+// contiguous runs of ceil(n / waves) over the grid's waves (one row per wave
+// when n is small; consecutive rows are read and prefetched from the same DRAM
+// neighbourhood). Otherwise a grid stride.
+__device__ __forceinline__ void wave_rows(bool runs, int64_t n, int wave, int64_t& rec,
+                                          int64_t& end, int64_t& step) {
+  const int64_t waves = (int64_t)gridDim.x * kWaves;
+  const int64_t id = (int64_t)blockIdx.x * kWaves + wave;
+  if (runs) {
+    const int64_t per = (n + waves - 1) / waves;
+    rec = id * per;
+    end = rec + per < n ? rec + per : n;
+    step = 1;
+  } else {
+    rec = id;
+    end = n;
+    step = waves;
+  }
+}
+
 template <bool kBf16, int kK, bool kPlanes>
 __global__ __launch_bounds__(256) void pack_rows_kernel(
     const void* __restrict__ x, int64_t stride, const float* __restrict__ weight, float eps,
@@ -391,19 +411,21 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(
     }
   }
   uint32_t hint = 126;  // threshold exponent of this wave's previous record (|x| ~ 2^-1)
-  const int64_t step = (int64_t)gridDim.x * kWaves;
-  int64_t rec = (int64_t)blockIdx.x * kWaves + wave;
+  // BF16 rows (1 KB): a contiguous run per wave (measured 3.7 % faster on the
+  // 1M-row bulk pack); FP32 rows (2 KB): the grid stride (1 % faster)
+  int64_t rec, end, step;
+  wave_rows(kBf16, n, wave, rec, end, step);
   RowRaw cur{};
   int32_t cur_slot = -1;
-  if (rec < n) {
+  if (rec < end) {
     cur = load_raw<kBf16>(x, rec, stride, lane);
     cur_slot = slots[rec];
   }
-  for (; rec < n; rec += step) {
+  for (; rec < end; rec += step) {
     // the next record's row and slot are in flight while this one is packed
     const RowRaw raw = cur;
     const int32_t slot = cur_slot;
-    if (rec + step < n) {
+    if (rec + step < end) {
       cur = load_raw<kBf16>(x, rec + step, stride, lane);
       cur_slot = slots[rec + step];
     }
@@ -516,8 +538,9 @@ __global__ __launch_bounds__(256) void native_store_kernel(
   float w[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) w[i] = weight[8 * lane + i];
-  for (int64_t rec = (int64_t)blockIdx.x * kWaves + wave; rec < n;
-       rec += (int64_t)gridDim.x * kWaves) {
+  int64_t rec0, end, step;
+  wave_rows(kBf16, n, wave, rec0, end, step);
+  for (int64_t rec = rec0; rec < end; rec += step) {
     const int64_t slot = slots[rec];
     if (slot < 0 || slot >= pool_rows) continue;
     int64_t pos = 0;
