@@ -227,7 +227,19 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = uniform(tid >> 6);
+  // Role index of this wave. A workgroup's six waves fill SIMDs 0..3 and then
+  // SIMDs 0 and 1 again, so two SIMDs hold two waves. By default the
+  // consumers are waves 0 and 1 and share those SIMDs with producers 2 and 3.
+  // Native workgroups of more than one stage put the consumers on waves 2 and
+  // 3 (a SIMD each) and the producers two per SIMD: the Native expansion is
+  // light enough to share a SIMD with another one (B=64 33.6 -> 31.4 us,
+  // B=128 x next-n 2 119.9 -> 109.1 us), the Packed one is not (35.5 -> 36.4),
+  // and single-stage splits gain nothing from it. Decided from the launch
+  // arguments alone, so the consumers' Q loads start at once.
+  const int wv_hw = uniform(tid >> 6);
+  const bool remap =
+      !kPacked && kHG == 1 && (a.topk + kPcStage - 1) / kPcStage > (int64_t)a.splits;
+  const int wv = !remap ? wv_hw : wv_hw == 2 ? 0 : wv_hw == 3 ? 1 : wv_hw < 2 ? wv_hw + 2 : wv_hw;
   const int64_t t = blockIdx.y;
   const int64_t head_wg = (int64_t)blockIdx.z * 16 * kHG;
   // a consumer's 16 heads (consumers 2 hg and 2 hg + 1 serve group hg)
