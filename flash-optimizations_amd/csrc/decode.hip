@@ -752,6 +752,33 @@ __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_swa_decode_pc_k
   decode_joint<false, kHG>(c4, swa);
 }
 
+// Butterfly over the wave's 64 lanes with the pairing of xor distances 1, 2,
+// 4, ..., 32 (quad permutes, the half-row and row mirrors -- in a butterfly
+// every lane of an aligned group already holds the same value, so the mirror
+// partner gives the xor partner's value -- then the 16- and 32-lane swaps):
+// the same additions as a shuffle-xor butterfly, without LDS round trips.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf, false));
+}
+template <bool kMax>
+__device__ __forceinline__ float wave_all(float x) {
+  auto op = [](float u, float v) { return kMax ? fmaxf(u, v) : u + v; };
+  x = op(x, dpp_f<0xB1>(x));   // quad_perm [1,0,3,2]
+  x = op(x, dpp_f<0x4E>(x));   // quad_perm [2,3,0,1]
+  x = op(x, dpp_f<0x141>(x));  // row_half_mirror
+  x = op(x, dpp_f<0x140>(x));  // row_mirror
+  const auto h = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = op(u2f(h[0]), u2f(h[1]));
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return op(u2f(q[0]), u2f(q[1]));
+}
+__device__ __forceinline__ float lane_of(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+
 // Merge split partials with the sink, for many rows: one wave per (token,
 // head) row, lane l owning coordinates 8l..8l+7. The partial loads of up to
 // kWaveBatch splits are issued together with the split LSEs (lane s holds
@@ -777,13 +804,9 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const float* __restri
   }
   const float ls = lane < splits ? ws_lse[(t * splits + lane) * heads + h] : -INFINITY;
   const float sink2 = sink ? sink[h] * kLog2e : -INFINITY;
-  float mz = fmaxf(ls, sink2);
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) mz = fmaxf(mz, __shfl_xor(mz, d, 64));
+  const float mz = wave_all<true>(fmaxf(ls, sink2));
   const float w = (mz != -INFINITY && lane < splits) ? exp2f(ls - mz) : 0.0f;
-  float z = w;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) z += __shfl_xor(z, d, 64);
+  const float z = wave_all<false>(w);
   f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < splits; s0 += kWaveBatch) {
     if (s0 > 0) {
@@ -798,8 +821,7 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const float* __restri
 #pragma unroll
     for (int u = 0; u < kWaveBatch; ++u) {
       const int sp = s0 + u;
-      const float wu = __shfl(w, sp < splits ? sp : 0, 64);
-      const float ww = sp < splits ? wu : 0.0f;
+      const float ww = sp < splits ? lane_of(w, sp) : 0.0f;
       a0 += ww * x[2 * u];
       a1 += ww * x[2 * u + 1];
     }
@@ -848,19 +870,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   }
   const float ls = lane < splits ? ws_lse[(t * splits + lane) * heads + h] : -INFINITY;
   const float sink2 = sink ? sink[h] * kLog2e : -INFINITY;
-  float mz = fmaxf(ls, sink2);
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) mz = fmaxf(mz, __shfl_xor(mz, d, 64));
+  const float mz = wave_all<true>(fmaxf(ls, sink2));
   const float w = (mz != -INFINITY && lane < splits) ? exp2f(ls - mz) : 0.0f;
-  float z = w;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) z += __shfl_xor(z, d, 64);
+  const float z = wave_all<false>(w);
   float acc = 0.0f;
 #pragma unroll
   for (int u = 0; u < kPerWave; ++u) {
     const int s = wave + 4 * u;
-    const float wu = __shfl(w, s < splits ? s : 0, 64);
-    acc += (s < splits ? wu : 0.0f) * x[u];
+    acc += (s < splits ? lane_of(w, s) : 0.0f) * x[u];
   }
   part[wave][lane] = acc;
   __syncthreads();
