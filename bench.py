@@ -10,13 +10,16 @@ Also reported on the same JSON line:
   roofline      dominant kernel's algorithmic bytes / HIP-event-timed duration
                 against MI355X's 8 TB/s HBM peak (traffic from the committed
                 rocprofv3 counter runs when available);
-  kernels       per-kernel timings (pack, reconstruct, reconstruct+RoPE);
+  kernels       per-kernel timings (pack from BF16 and from FP32 input,
+                reconstruct, reconstruct + RoPE);
   decode        Direct packed vs Native sparse decode: batch 1 (16 heads, top-k
                 2048, 8192-record context), batch 64 (log-uniform 4k-128k token
                 contexts), batch 128 x next-n 2 at 128k-token contexts on a
-                pool sized to most of HBM (capacity case);
-  cpu_baseline  the CPU oracle (single thread) on a bounded sample of the
-                same workload, timed on this host.
+                pool sized to most of HBM (capacity case), and the reference's
+                own decode shapes (H64/H128 x B8/B16, top-k 512, window rows);
+  cpu_baseline  the CPU oracle's pack + reconstruct on a bounded sample of the
+                same workload, and its decode at batch 1 and 64, each on one
+                thread and on all of this host's cores.
 
 ``--keep-count K`` runs the bulk leg on a survivor profile other than 256
 (64..448 in steps of 64; records of K + 72 bytes); the decode leg always reads
