@@ -80,7 +80,7 @@ struct DecodeArgs {
   float scale_log2;
   int64_t q_len;
   int64_t heads;
-  int chunk;       // records per split (multiple of 32, <= kPcMaxChunk)
+  int chunk;       // records per split (multiple of 32)
   int splits;      // splits of this list (workgroups along x)
   int ws_splits;   // partial slots per row in the workspace; 0: finalise in place
   int ws_base;     // slot of this list's split 0
@@ -117,6 +117,26 @@ __device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
   __builtin_amdgcn_global_load_lds(src, (lds_void*)(uintptr_t)__builtin_amdgcn_readfirstlane(lds),
                                    4, 0, 0);
 }
+// A 4-byte global -> LDS copy issued from inline assembly (M0 set and read in
+// the same block, one wait state between). The compiler then sees no LDS DMA
+// in flight in the issuing wave and adds no waits of its own before the
+// wave's later LDS reads (before a ds_read_b64_tr_b16 it would otherwise wait
+// for every outstanding copy); the wave waits for its copies explicitly.
+__device__ __forceinline__ void dma4_opaque(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :
+               : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory", "m0");
+}
+// This lane's index from instructions the compiler cannot hoist: values
+// derived from it are computed where they are used, not kept live across a
+// loop whose registers are taken.
+__device__ __forceinline__ int opaque_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // Workgroup barrier for LDS data written by ordinary stores: this wave's LDS
 // operations complete, then all waves meet. No memory-model fence: a release
 // fence would also wait for every outstanding global load, including the
@@ -186,12 +206,18 @@ struct PcShared {
   using G = PcGeo<kPacked>;
   uint8_t raw[kPcProducers][G::kDepth][G::kBuf];  // copy ring (LDS address 0)
   uint16_t ktile[kPcRing][kT * kPcKPitch];
-  // per record slot of the split: pool row address, or (Q address | 1) for an
-  // invalid record or a slot past the end (a readable stand-in source, odd so
-  // that bit 0 marks it); Packed: RoPE row address (row 0 of the table for an
-  // invalid record, Q without a table)
+  // per record slot of the split, a ring of kPcMaxChunk entries (record i at
+  // i % kPcMaxChunk; splits of more than kPcMaxChunk records refill it as they
+  // go): pool row address, or (Q address | 1) for an invalid record or a slot
+  // past the end (a readable stand-in source, odd so that bit 0 marks it);
+  // Packed: RoPE row address (row 0 of the table for an invalid record, Q
+  // without a table)
   uint64_t row_tab[kPcMaxChunk];
   uint64_t aux_tab[kPacked ? kPcMaxChunk : 1];
+  // long splits: the records' top-k entries and block-table entries of the
+  // next stages, copied in ahead of the table entries made from them
+  int32_t idx_ring[3][64];
+  int32_t bt_ring[3][64];
   uint64_t sel_tab[kPacked ? 256 : 1];
   float mrg[2 * kPcMaxGroups][2][16];  // consumers' (reference, seen) maxima per head
 };
@@ -285,32 +311,84 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     sel_tab[e] = sel;
   }
   const uint64_t stand_in = (uint64_t)a.q | 1u;
-  for (int i = tid; i < kPcMaxChunk; i += kPcThreads) {
-    bool ok = false;
-    int64_t r = 0, page = 0;
-    if (i < n) {
-      r = a.indices[t * a.topk + k0 + i];
-      if (a.block_table) {  // logical record of request b
-        ok = r >= 0 && r < seqlen && (r >> 6) < a.max_blocks;
-        page = ok ? a.block_table[b * a.bt_stride + (r >> 6)] : -1;
-      } else {  // pool slot
-        ok = r >= 0;
-        page = r >> 6;
-      }
-      ok = ok && page >= 0 && page < a.pool_pages && page * 64 + (r & 63) < a.pool_rows;
-      if (kPacked && a.freqs) ok = ok && r * 4 < a.freq_rows;
+  const bool paged = a.block_table != nullptr;
+  // whether logical record r of request b has a block-table entry to read
+  auto in_table = [&](int64_t r) { return r >= 0 && r < seqlen && (r >> 6) < a.max_blocks; };
+  // table entry of record slot i from its top-k entry r (< 0: none) and, for
+  // a paged pool, its block-table entry pv (meaningful only when in_table(r))
+  auto put_entry = [&](int i, int64_t r, int64_t pv) {
+    bool ok;
+    int64_t page;
+    if (paged) {  // logical record of request b
+      ok = in_table(r);
+      page = ok ? pv : -1;
+    } else {  // pool slot
+      ok = r >= 0;
+      page = r >> 6;
     }
+    ok = ok && page >= 0 && page < a.pool_pages && page * 64 + (r & 63) < a.pool_rows;
+    if (kPacked && a.freqs) ok = ok && r * 4 < a.freq_rows;
     // planes: the record's values row (16-byte aligned); its bitmap and scale
     // rows sit at a quarter and a 32nd of the values offset in their planes
     const uint8_t* pg = kPlanes ? a.pool + (ok ? page : 0) * 64 * kCodeBytes
                                 : a.pool + (ok ? page : 0) * G::kPage;
-    row_tab[i] = ok ? (uint64_t)(pg + (r & 63) * (kPlanes ? kCodeBytes : G::kData)) |
-                          (kPacked ? 0 : (uint64_t)(r & 63) << 58)
-                    : stand_in;
-    if (kPacked) aux_tab[i] = a.freqs ? (uint64_t)(a.freqs + (ok ? r : 0) * 4 * 64) : (uint64_t)a.q;
-  }
+    const int slot = i & (kPcMaxChunk - 1);
+    row_tab[slot] = ok ? (uint64_t)(pg + (r & 63) * (kPlanes ? kCodeBytes : G::kData)) |
+                             (kPacked ? 0 : (uint64_t)(r & 63) << 58)
+                       : stand_in;
+    if (kPacked) aux_tab[slot] = a.freqs ? (uint64_t)(a.freqs + (ok ? r : 0) * 4 * 64) : (uint64_t)a.q;
+  };
+  // the first kPcMaxChunk slots, read directly by all threads
+  auto build_table = [&]() {
+    for (int i = tid; i < kPcMaxChunk; i += kPcThreads) {
+      int64_t r = -1, pv = 0;
+      if (i < n) {
+        r = a.indices[t * a.topk + k0 + i];
+        if (paged && in_table(r)) pv = a.block_table[b * a.bt_stride + (r >> 6)];
+      }
+      put_entry(i, r, pv);
+    }
+  };
+  build_table();
   wait_vm();
   __syncthreads();
+
+  // Splits of more than kPcMaxChunk records: consumer 0 refills the table
+  // ring ahead of the producers, after its MFMA work of each step s. It
+  // copies the top-k entries of stage s + 6 into LDS, copies the block-table
+  // entries of stage s + 5 (from the top-k entries copied a step earlier), and
+  // writes the table entries of stage s + 4, whose copies the producers issue
+  // at step s + 1, after the barrier. Slot i % kPcMaxChunk then belongs to
+  // stage i / kPcStage - 16, consumed at step s - 11. The copies go through
+  // inline assembly with this wave's own waits, so the compiler adds none
+  // before the MFMA loop's transposed LDS reads.
+  constexpr int kRingStages = kPcMaxChunk / kPcStage;
+  const bool long_split = stages > kRingStages;
+  auto refill = [&](int s) {
+    wait_vm();  // this wave's copies of the previous step have landed
+    const int ln = opaque_lane();
+    int q = s + 4;
+    if (q >= kRingStages && q < stages && ln < kPcStage) {
+      const int i = q * kPcStage + ln;
+      const int64_t r = i < n ? (int64_t)sm->idx_ring[q % 3][ln] : -1;
+      put_entry(i, r, sm->bt_ring[q % 3][ln]);
+    }
+    q = s + 5;
+    if (q >= kRingStages && q < stages) {
+      const int i = q * kPcStage + ln;
+      const int64_t r = ln < kPcStage && i < n ? (int64_t)sm->idx_ring[q % 3][ln] : -1;
+      const int32_t* src = paged && in_table(r) ? a.block_table + (b * a.bt_stride + (r >> 6))
+                                                : (const int32_t*)a.q;
+      dma4_opaque(src, lds_addr(&sm->bt_ring[q % 3][0]));
+    }
+    q = s + 6;
+    if (q >= kRingStages && q < stages) {
+      const int i = q * kPcStage + ln;
+      const int32_t* src = ln < kPcStage && i < n ? a.indices + (t * a.topk + k0 + i)
+                                                  : (const int32_t*)a.q;
+      dma4_opaque(src, lds_addr(&sm->idx_ring[q % 3][0]));
+    }
+  };
 
   // Overflow test on the consumers' published (reference, seen) maxima: a
   // workgroup-uniform decision every wave takes from LDS.
@@ -345,12 +423,12 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
       for (int j = 0; j < G::kCopies; ++j) {
         const int c = lane + 64 * j;
         const int r = c < G::kRecPieces ? c / G::kPieces : (c - G::kRecPieces) & 7;
-        const int idx = min(rec0 + r, kPcMaxChunk - 1);
+        const int idx = (rec0 + r) & (kPcMaxChunk - 1);
         rw[j] = c >= G::kPieceCount ? (uint64_t)a.q
                 : (kPacked && c >= G::kRecPieces) ? aux_tab[idx] : row_tab[idx];
       }
       uint64_t srow = 0;
-      if (!kPacked) srow = row_tab[min(rec0 + ((lane >> 1) & 7), kPcMaxChunk - 1)];
+      if (!kPacked) srow = row_tab[(rec0 + ((lane >> 1) & 7)) & (kPcMaxChunk - 1)];
 #pragma unroll
       for (int j = 0; j < G::kCopies; ++j) {
         const int c = lane + 64 * j;
@@ -397,7 +475,7 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     auto head = [&](int s, auto bufc, Head& h) {
       constexpr int B = decltype(bufc)::value;
       const uint8_t* st = &raw[p][B][0] + pi * G::kPitch;
-      h.row = row_tab[s * kPcStage + 8 * p + pi];
+      h.row = row_tab[(s * kPcStage + 8 * p + pi) & (kPcMaxChunk - 1)];
       // a record staged from an odd pool row starts 8 bytes in
 #pragma unroll
       for (int e = 0; e < 4; ++e) h.w[e] = *(const uint32_t*)(st + kCodeBytes + 8 * pw + 4 * e);
@@ -490,7 +568,7 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
         // lane (record i, word w) converts the 64 coordinates of word w; piece
         // pairs in the order (c + w / 2) % 4 keep a record's lanes on distinct banks
         const int ni = lane >> 3, nw = lane & 7;
-        const bool nvalid = !(row_tab[s * kPcStage + 8 * p + ni] & 1u);
+        const bool nvalid = !(row_tab[(s * kPcStage + 8 * p + ni) & (kPcMaxChunk - 1)] & 1u);
         const uint8_t* const rb = &raw[p][B][0];
         const uint8_t* nst = rb + ni * G::kPitch;
         uint16_t* const nrow =
@@ -565,6 +643,11 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
       const bool redo = redo_pass(mtrue);
       __syncthreads();
       if (!redo) break;
+      if (long_split) {  // the ring holds the last stages: rebuild the first ones
+        build_table();
+        wait_vm();
+        __syncthreads();
+      }
     }
     return;
   }
@@ -588,7 +671,8 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
   auto consume = [&](int sa, int sb, int tile0) {
     const uint16_t* kta = &ktile[sa][0];
     const uint16_t* ktb = &ktile[sb][0];
-    const uint64_t ra = row_tab[tile0 + col], rb = row_tab[tile0 + kT + col];
+    const uint64_t ra = row_tab[(tile0 + col) & (kPcMaxChunk - 1)];
+    const uint64_t rb = row_tab[(tile0 + kT + col) & (kPcMaxChunk - 1)];
     const uint64_t va = __ballot(lane < kT && !(ra & 1u));
     const uint64_t vb = __ballot(lane < kT && !(rb & 1u));
     const int ko = col * kPcKPitch + kchunk(g);  // chunk 4 ks + g at ko + 16 ks
@@ -664,6 +748,11 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     for (int s = 0; s <= stages; ++s) {
       block_sync_lds();  // stage s - 1 in the ring
       if (s >= 1) consume((2 * s - 2) % kPcRing, (2 * s - 1) % kPcRing, (s - 1) * kPcStage);
+      if (long_split && wv == 0) {  // outside the MFMA work's scheduling groups
+        __builtin_amdgcn_sched_barrier(0);
+        refill(s);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     m_seen = fmaxf(m_seen, __shfl_xor(m_seen, 16, 64));
     m_seen = fmaxf(m_seen, __shfl_xor(m_seen, 32, 64));
@@ -677,6 +766,11 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     __syncthreads();
     if (!redo) break;
     m_ref = __shfl(mtrue, col, 64);  // reference: the true max
+    if (long_split) {  // as the producers: the first stages' entries again
+      build_table();
+      wait_vm();
+      __syncthreads();
+    }
   }
 
   // ---- finalise this consumer's half of O ----
@@ -900,9 +994,11 @@ struct Plan {
 };
 
 // Split plan: about one workgroup per CU (256 CUs), whole 32-record stages per
-// split, at most kPcMaxChunk records per split and max_splits splits (the
-// combine merges at most kMaxSplits partial slots per row, the window rows'
-// slot included).
+// split and at most max_splits splits (the combine merges at most kMaxSplits
+// partial slots per row, the window rows' slot included). A split may hold
+// more than kPcMaxChunk records (its table ring is refilled as it goes), so
+// a batch that fills the round on its own takes one split per token: one
+// round of workgroups and no partials to merge.
 // 16-head groups per workgroup. Two groups share every expanded record (half
 // the expansion work per head) but double a workgroup's consumer work; that
 // pays once 16-head workgroups alone would fill the GPU's round of about 256
@@ -920,10 +1016,8 @@ Plan plan_pc(int64_t tokens, int64_t heads, int64_t topk, int64_t max_splits = k
   int64_t splits = base > 0 ? (256 + base - 1) / base : 1;
   // the window rows' workgroups (one per token and head block) share the round
   if (window && base > 0) splits = 256 / base - 1;
-  const int64_t min_splits = (topk + kPcMaxChunk - 1) / kPcMaxChunk;
   if (splits > stages) splits = stages;
   if (splits > max_splits) splits = max_splits;
-  if (splits < min_splits) splits = min_splits;
   if (splits < 1) splits = 1;
   int64_t chunk_stages = (stages + splits - 1) / splits;
   if (chunk_stages < 1) chunk_stages = 1;

@@ -1,5 +1,7 @@
 """GPU parity at the edges the shared parity suite leaves open.
 
+* Long splits (one split per token over 1,504 records): the record table
+  refilled as a split streams, with the second pass of a wide score range.
 * Capacity decode (batch 128 x 2 query tokens, top-k 2048, 32,768-record
   contexts) on a pool of 450,000 pages (9.4 GB), so record offsets pass 2^32:
   sampled requests against the oracle, plus pack and reconstruct at the high
@@ -332,6 +334,30 @@ def test_pack_fp32_full_precision_threshold_mantissas_and_ties():
     want = ref.reshape(-1, 328)
     bad = np.nonzero((got[slots[pick]] != want[slots[pick]]).any(axis=1))[0]
     assert bad.size == 0, f"{bad.size} records differ, first record {int(pick[bad[0]])}"
+
+
+# ---- long splits: a split's record table refilled while it streams ------------------------
+
+@pytest.mark.parametrize("packed", [True, False], ids=["direct", "native"])
+def test_decode_long_splits_refilled_table_and_second_pass(packed):
+    """128 requests x 2 query tokens x 16 heads (256 token x 16-head blocks, so
+    one split per token) at top-k 1504: each split streams 47 stages of 32
+    records, far past the 512 table entries a workgroup holds, so the entries
+    are refilled ring-wise as the split streams. Lengths 1504, 1000, 513, 512,
+    31 and 0 end the split inside, at and before the table's first wrap; q is
+    scaled so later tiles exceed the first tile's max and the split runs a
+    second pass over a rebuilt table. Every row is checked against the oracle."""
+    banner(f"decode long splits packed={packed}")
+    ctx = syn.log_uniform_contexts(128, 6400, 12000, 481)
+    topk = 1504
+    c = build_decode_case(ctx, q_len=2, heads=16, topk=topk, seed=481, packed=packed)
+    assert remnant.get_decode_metadata(256, 16, topk)[0] == 1
+    lens = c["lens"].reshape(-1)
+    lens[1:6] = [1000, 513, 512, 31, 0]
+    c["q"] = (c["q"].float() * 300).to(torch.bfloat16)
+    out, lse = run_decode(c)
+    ref, ref_lse = oracle_decode(c)
+    per_row_check(out, ref, lse, ref_lse)
 
 
 # ---- capacity decode on a pool above 8 GB ---------------------------------------------------

@@ -78,19 +78,23 @@ def test_noalloc_decode_equals_workspace_decode_on_two_calls():
 def test_noalloc_decode_refuses_split_plans_beyond_its_array():
     banner("noalloc: oversized plan refused")
     lib = _lib.load()
-    # 100 tokens x 128 heads x 64 splits of 2 KiB partial rows: far beyond 32 MiB
-    splits, need = remnant.get_decode_metadata(100, 128, 32768)
-    assert need > (32 << 20)
-    q = torch.zeros((100, 1, 128, 512), dtype=torch.bfloat16, device=DEV)
+    # 1,024 tokens x 16 heads: one C4 split each plus the window rows' slot,
+    # 2 partial rows of 2 KiB per (token, head): 64 MiB, beyond the 32 MiB array
+    tokens, heads, topk, wtop = 1024, 16, 512, 64
+    slots, need = remnant.get_decode_metadata(tokens, heads, topk, wtop)
+    assert slots == 2 and need > (32 << 20)
+    q = torch.zeros((tokens, 1, heads, 512), dtype=torch.bfloat16, device=DEV)
     pool = remnant.LatentPool(1, device=DEV).layer()
-    bt = torch.zeros((100, 1), dtype=torch.int32, device=DEV)
-    idx = torch.full((100, 1, 32768), -1, dtype=torch.int32, device=DEV)
+    swa_pool = remnant.LatentPool(1, fmt="native", device=DEV).layer()
+    bt = torch.zeros((tokens, 1), dtype=torch.int32, device=DEV)
+    idx = torch.full((tokens, 1, topk), -1, dtype=torch.int32, device=DEV)
+    widx = torch.full((tokens, 1, wtop), -1, dtype=torch.int32, device=DEV)
     out = torch.full_like(q, 3.0)
-    lse = torch.zeros((100, 1, 128), dtype=torch.float32, device=DEV)
+    lse = torch.zeros((tokens, 1, heads), dtype=torch.float32, device=DEV)
     st = lib.rm_remnant_sparse_decode_swa_noalloc_fwd(
-        q.data_ptr(), 100, 1, 128, pool.data_ptr(), 1, bt.data_ptr(), 1, 1, None, idx.data_ptr(),
-        32768, None, None, 0, None, 0, None, None, None, 0, 0.1, out.data_ptr(), lse.data_ptr(),
-        torch.cuda.current_stream().cuda_stream)
+        q.data_ptr(), tokens, 1, heads, pool.data_ptr(), 1, bt.data_ptr(), 1, 1, None,
+        idx.data_ptr(), topk, None, swa_pool.data_ptr(), 1, widx.data_ptr(), wtop, None, None,
+        None, 0, 0.1, out.data_ptr(), lse.data_ptr(), torch.cuda.current_stream().cuda_stream)
     assert st == -5
     torch.cuda.synchronize()
     assert torch.all(out.float() == 3.0)  # nothing was launched
