@@ -121,12 +121,17 @@ __device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
 // the same block, one wait state between). The compiler then sees no LDS DMA
 // in flight in the issuing wave and adds no waits of its own before the
 // wave's later LDS reads (before a ds_read_b64_tr_b16 it would otherwise wait
-// for every outstanding copy); the wave waits for its copies explicitly.
+// for every outstanding copy); the wave waits for its copies explicitly. M0 is
+// a reserved register the compiler may keep a value in across the block, so
+// the block saves and restores it (the copy reads M0 when it issues).
 __device__ __forceinline__ void dma4_opaque(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :
-               : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory", "m0");
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds))
+      : "memory");
 }
 // This lane's index from instructions the compiler cannot hoist: values
 // derived from it are computed where they are used, not kept live across a
@@ -237,7 +242,7 @@ __device__ __forceinline__ float max_over_rows(float x) {
 // One workgroup's share: split `split` of list `a` (a C4 top-k list through
 // the block table, or with a.block_table == nullptr a list of pool slots), for
 // kHG groups of 16 heads: every expanded record serves all of them.
-template <bool kPacked, int kHG, bool kPlanes = false>
+template <bool kPacked, int kHG, bool kPlanes = false, bool kLong = false>
 __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>* sm,
                                           const int split) {
   static_assert(kPacked || !kPlanes, "planes hold Packed records");
@@ -363,7 +368,7 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
   // inline assembly with this wave's own waits, so the compiler adds none
   // before the MFMA loop's transposed LDS reads.
   constexpr int kRingStages = kPcMaxChunk / kPcStage;
-  const bool long_split = stages > kRingStages;
+  const bool long_split = kLong && stages > kRingStages;
   auto refill = [&](int s) {
     wait_vm();  // this wave's copies of the previous step have landed
     const int ln = opaque_lane();
@@ -815,35 +820,63 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
   }
 }
 
-template <int kHG, bool kPlanes>
+// kLong: splits may run past kPcMaxChunk records (the table ring refill),
+// compiled apart so that shorter splits carry none of its code.
+template <int kHG, bool kPlanes, bool kLong>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void packed_decode_pc_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[sizeof(PcShared<true>)];
-  decode_pc<true, kHG, kPlanes>(a, reinterpret_cast<PcShared<true>*>(smem), blockIdx.x);
+  decode_pc<true, kHG, kPlanes, kLong>(a, reinterpret_cast<PcShared<true>*>(smem), blockIdx.x);
 }
-template <int kHG>
+template <int kHG, bool kLong>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_decode_pc_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[sizeof(PcShared<false>)];
-  decode_pc<false, kHG>(a, reinterpret_cast<PcShared<false>*>(smem), blockIdx.x);
+  decode_pc<false, kHG, false, kLong>(a, reinterpret_cast<PcShared<false>*>(smem), blockIdx.x);
 }
 // C4 list and window rows in one launch: workgroups x < c4.splits take a C4
-// split, the last column the window rows (Native records).
-template <bool kPacked, int kHG, bool kPlanes = false>
+// split, the last column the window rows (Native records, one short split).
+template <bool kPacked, int kHG, bool kPlanes, bool kLong>
 __device__ __forceinline__ void decode_joint(const DecodeArgs& c4, const DecodeArgs& swa) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kPcSmemBytes];
   if ((int)blockIdx.x < c4.splits)
-    decode_pc<kPacked, kHG, kPlanes>(c4, reinterpret_cast<PcShared<kPacked>*>(smem), blockIdx.x);
+    decode_pc<kPacked, kHG, kPlanes, kLong>(c4, reinterpret_cast<PcShared<kPacked>*>(smem),
+                                            blockIdx.x);
   else
     decode_pc<false, kHG>(swa, reinterpret_cast<PcShared<false>*>(smem), 0);
 }
-template <int kHG, bool kPlanes>
+template <int kHG, bool kPlanes, bool kLong>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void packed_swa_decode_pc_kernel(
     DecodeArgs c4, DecodeArgs swa) {
-  decode_joint<true, kHG, kPlanes>(c4, swa);
+  decode_joint<true, kHG, kPlanes, kLong>(c4, swa);
 }
-template <int kHG>
+template <int kHG, bool kLong>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_swa_decode_pc_kernel(
     DecodeArgs c4, DecodeArgs swa) {
-  decode_joint<false, kHG>(c4, swa);
+  decode_joint<false, kHG, false, kLong>(c4, swa);
+}
+
+// The workgroup kernel for a format, storage layout, head grouping and split length.
+using SplitKernel = void (*)(DecodeArgs);
+using JointKernel = void (*)(DecodeArgs, DecodeArgs);
+template <bool kPacked, bool kLong>
+SplitKernel split_kernel(bool planes, int hg) {
+  if constexpr (!kPacked)
+    return hg == 2 ? native_decode_pc_kernel<2, kLong> : native_decode_pc_kernel<1, kLong>;
+  else if (planes)
+    return hg == 2 ? packed_decode_pc_kernel<2, true, kLong> : packed_decode_pc_kernel<1, true, kLong>;
+  else
+    return hg == 2 ? packed_decode_pc_kernel<2, false, kLong>
+                   : packed_decode_pc_kernel<1, false, kLong>;
+}
+template <bool kPacked, bool kLong>
+JointKernel joint_kernel(bool planes, int hg) {
+  if constexpr (!kPacked)
+    return hg == 2 ? native_swa_decode_pc_kernel<2, kLong> : native_swa_decode_pc_kernel<1, kLong>;
+  else if (planes)
+    return hg == 2 ? packed_swa_decode_pc_kernel<2, true, kLong>
+                   : packed_swa_decode_pc_kernel<1, true, kLong>;
+  else
+    return hg == 2 ? packed_swa_decode_pc_kernel<2, false, kLong>
+                   : packed_swa_decode_pc_kernel<1, false, kLong>;
 }
 
 // Butterfly over the wave's 64 lanes with the pairing of xor distances 1, 2,
@@ -1136,6 +1169,7 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   const int hg = head_groups(tokens, heads);
   const dim3 block(hg == 2 ? PcRoles<2>::kThreads : PcRoles<1>::kThreads);
   const unsigned zblocks = (unsigned)(heads / (16 * hg));
+  const bool lng = plan.chunk > kPcMaxChunk;
   if (w.topk > 0) {
     // the window rows are one more split, read by the Native path of the same launch
     DecodeArgs b = a;
@@ -1155,23 +1189,13 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
     b.splits = 1;
     b.ws_base = plan.splits;
     const dim3 grid((unsigned)slots, (unsigned)tokens, zblocks);
-    void (*kern)(DecodeArgs, DecodeArgs);
-    if (!kPacked)
-      kern = hg == 2 ? native_swa_decode_pc_kernel<2> : native_swa_decode_pc_kernel<1>;
-    else if (src.planes())
-      kern = hg == 2 ? packed_swa_decode_pc_kernel<2, true> : packed_swa_decode_pc_kernel<1, true>;
-    else
-      kern = hg == 2 ? packed_swa_decode_pc_kernel<2, false> : packed_swa_decode_pc_kernel<1, false>;
+    const JointKernel kern = lng ? joint_kernel<kPacked, true>(src.planes(), hg)
+                                 : joint_kernel<kPacked, false>(src.planes(), hg);
     hipLaunchKernelGGL(kern, grid, block, 0, s, a, b);
   } else {
     const dim3 grid((unsigned)plan.splits, (unsigned)tokens, zblocks);
-    void (*kern)(DecodeArgs);
-    if (!kPacked)
-      kern = hg == 2 ? native_decode_pc_kernel<2> : native_decode_pc_kernel<1>;
-    else if (src.planes())
-      kern = hg == 2 ? packed_decode_pc_kernel<2, true> : packed_decode_pc_kernel<1, true>;
-    else
-      kern = hg == 2 ? packed_decode_pc_kernel<2, false> : packed_decode_pc_kernel<1, false>;
+    const SplitKernel kern = lng ? split_kernel<kPacked, true>(src.planes(), hg)
+                                 : split_kernel<kPacked, false>(src.planes(), hg);
     hipLaunchKernelGGL(kern, grid, block, 0, s, a);
   }
   if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
