@@ -9,14 +9,15 @@
 //   out = sum_j exp(l_j) K_j / Z, lse = ln Z.
 //
 // Work split. A workgroup of six waves owns (split, token, 16-head block) and
-// walks its share of the top-k list (<= 512 records) in stages of 32 records:
+// walks its share of the top-k list in stages of 32 records:
 //   * record metadata (index -> block table -> page/row, validity) for the
 //     share is resolved once into LDS; invalid records and slots past the end
 //     point at a readable stand-in and are masked to zero;
 //   * four producer waves each own 8 records of every stage. They copy the
-//     record rows (and for Packed the RoPE rows) HBM -> LDS with
-//     global_load_lds three stages ahead -- a fixed number of copies per stage,
-//     so their waits are compile-time vmcnt values -- and expand them into
+//     record rows HBM -> LDS with global_load_lds three stages ahead (Packed:
+//     each lane loads the 32 bytes of RoPE row it rotates into registers two
+//     stages ahead, in the same in-order load stream) -- a fixed number of
+//     loads per stage, so their waits are compile-time vmcnt values -- and expand them into
 //     dense BF16 K rows in a four-slot LDS ring: v_perm places the kept E4M3
 //     codes (zeros for pruned coordinates) from a 256-entry selector table,
 //     v_cvt_scalef32_pk_bf16_fp8 applies the UE8M0 scale, the tail pairs are
@@ -133,6 +134,22 @@ __device__ __forceinline__ void dma4_opaque(const void* src, uint32_t lds) {
       : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds))
       : "memory");
 }
+// A 16-byte global load the compiler does not track: it adds no waits of its
+// own for it (the extra load in the in-order stream only lengthens the
+// compiler's other waits). The caller reads dst only through wait_vm_regs,
+// whose operands tie the registers to the wait, and reads every value it
+// loads that way, so no register is handed out again while a load into it is
+// in flight.
+__device__ __forceinline__ void load16_untracked(const void* src, f32x4& dst) {
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(dst) : "v"(src) : "memory");
+}
+// Wait until at most N global loads of this wave are outstanding; x and y are
+// read after the wait.
+template <int N>
+__device__ __forceinline__ void wait_vm_regs(f32x4& x, f32x4& y) {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N) : "memory");
+}
 // This lane's index from instructions the compiler cannot hoist: values
 // derived from it are computed where they are used, not kept live across a
 // loop whose registers are taken.
@@ -193,13 +210,13 @@ struct PcGeo {
   static constexpr int kPieces = kPacked ? 21 : kNativeDataBytes / 16;  // 16-B pieces per record
   static constexpr int kPitch = 16 * kPieces;                          // staged record pitch
   static constexpr int kRecPieces = 8 * kPieces;                       // one producer's 8 records
-  // Packed: the 8 RoPE rows follow, piece k of record r at slot 8 k + r
-  static constexpr int kFreqAt = 16 * kRecPieces;
-  static constexpr int kPieceCount = kRecPieces + (kPacked ? 8 * 16 : 0);
+  static constexpr int kPieceCount = kRecPieces;
   static constexpr int kCopies = (kPieceCount + 63) / 64;              // 16-B copies per stage
   static constexpr int kScaleAt = 1024 * kCopies;                      // Native: scale rows
   static constexpr int kBuf = kScaleAt + (kPacked ? 0 : 256);          // bytes per stage buffer
-  static constexpr int kLoads = kCopies + (kPacked ? 0 : 1);           // global loads per stage
+  // global loads per stage: the copies, plus the Native scale row or the two
+  // Packed RoPE loads
+  static constexpr int kLoads = kCopies + (kPacked ? 2 : 1);
   static constexpr int kDepth = 4;  // copy ring buffers (the step loop is unrolled by 4)
 };
 
@@ -427,10 +444,9 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
 #pragma unroll
       for (int j = 0; j < G::kCopies; ++j) {
         const int c = lane + 64 * j;
-        const int r = c < G::kRecPieces ? c / G::kPieces : (c - G::kRecPieces) & 7;
+        const int r = c < G::kRecPieces ? c / G::kPieces : 0;
         const int idx = (rec0 + r) & (kPcMaxChunk - 1);
-        rw[j] = c >= G::kPieceCount ? (uint64_t)a.q
-                : (kPacked && c >= G::kRecPieces) ? aux_tab[idx] : row_tab[idx];
+        rw[j] = c >= G::kPieceCount ? (uint64_t)a.q : row_tab[idx];
       }
       uint64_t srow = 0;
       if (!kPacked) srow = row_tab[(rec0 + ((lane >> 1) & 7)) & (kPcMaxChunk - 1)];
@@ -448,8 +464,8 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
           } else {
             src = (rw[j] & (kPacked ? ~(uint64_t)15 : kAddrMask & ~(uint64_t)15)) + 16 * piece;
           }
-        } else {  // Packed RoPE piece (c - kRecPieces) / 8, or a filler lane
-          src = rw[j] + 16 * ((c - G::kRecPieces) >> 3);
+        } else {  // a filler lane
+          src = rw[j];
         }
         dma16((const void*)src, base + 1024 * j);
       }
@@ -540,6 +556,25 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
                   cvt2<true>(hi, gt.scale)};
       }
     };
+    // RoPE rows: lane (i, j) loads bytes 32 j .. 32 j + 31 of record i's row
+    // (the (cos, sin) of pairs 4j..4j+3) into a two-stage register ring, two
+    // stages ahead, after the stage's copies. For stages past the end it loads
+    // from Q (the loads per stage stay fixed).
+    f32x4 rope_r[2][2];
+    auto issue_rope = [&](int s, auto slotc) {
+      constexpr int S = decltype(slotc)::value;
+      const uint64_t entry = aux_tab[(s * kPcStage + 8 * p + pi) & (kPcMaxChunk - 1)];
+      const uint64_t row = s < stages ? entry : (uint64_t)a.q;
+      load16_untracked((const void*)(row + 32 * pw), rope_r[S][0]);
+      load16_untracked((const void*)(row + 32 * pw + 16), rope_r[S][1]);
+    };
+    // loads issued after the RoPE loads of stage s when stage s is rotated: the
+    // copies of stage s + 2, the RoPE loads of stage s + 1, the copies of s + 3
+    constexpr int kRopeLag = 2 * G::kCopies + 2;
+    auto rope_ready = [&](auto slotc) {
+      constexpr int S = decltype(slotc)::value;
+      wait_vm_regs<kRopeLag>(rope_r[S][0], rope_r[S][1]);
+    };
     // tail: lane (i, j) rotates pairs 4j..4j+3 of record i (BF16 in, BF16 out);
     // an invalid record's tail is zero and its stand-in RoPE row finite; without
     // a table the rotation is the identity
@@ -549,9 +584,9 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
       uint16_t* const tail = &ktile[(2 * s + (p >> 1)) % kPcRing][0] +
                              (8 * (p & 1) + pi) * kPcKPitch + kchunk(kNopeDim / 8 + pw);
       const u32x4 v = *(const u32x4*)tail;
-      const uint8_t* fb = &raw[p][B][0] + G::kFreqAt + 16 * pi;
-      const f32x4 f0 = *(const f32x4*)(fb + 256 * pw);        // piece 2j
-      const f32x4 f1 = *(const f32x4*)(fb + 256 * pw + 128);  // piece 2j + 1
+      rope_ready(std::integral_constant<int, B & 1>{});
+      const f32x4 f0 = rope_r[B & 1][0];
+      const f32x4 f1 = rope_r[B & 1][1];
       float x8[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -612,9 +647,10 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     // ring buffer of each step is fixed).
     auto step = [&](int s, auto bufc) {
       constexpr int B = decltype(bufc)::value;
-      // this wave's loads for stage s are done once at most those of the later
-      // D - 2 stages remain outstanding
-      wait_vm_upto<(D - 2) * G::kLoads>();
+      // this wave's copies of stage s are done once at most the loads issued
+      // after them remain outstanding: the later D - 2 stages' loads (Packed:
+      // and the RoPE loads of stage s - 1, issued right after the copies)
+      wait_vm_upto<(D - 2) * G::kLoads + (kPacked ? 2 : 0)>();
       wave_lds_sync();
       block_sync_lds();  // ring slots of stage s free (consumers are on stage s - 1)
       issue_stage(s + D - 1, std::integral_constant<int, (B + D - 1) % D>{});  // past the end: fillers
@@ -629,13 +665,25 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
         } else {
           produce_native(s, bufc);
         }
+      } else if constexpr (kPacked) {
+        rope_ready(std::integral_constant<int, B & 1>{});  // read, unused
       }
+      if constexpr (kPacked) issue_rope(s + 2, std::integral_constant<int, B & 1>{});
     };
 
     for (int pass = 0; pass < 2; ++pass) {
+      // the loads of steps -3 .. -1: copies of stages 0..2, each followed by
+      // two RoPE loads (stage -1: two copies of Q into the idle ring buffer 3)
       issue_stage(0, std::integral_constant<int, 0>{});
+      if constexpr (kPacked) {
+        const uint32_t idle = lds_addr(&raw[p][D - 1][0]);
+        dma16(a.q, idle);
+        dma16(a.q, idle + 1024);
+      }
       issue_stage(1, std::integral_constant<int, 1>{});
+      if constexpr (kPacked) issue_rope(0, std::integral_constant<int, 0>{});
       issue_stage(2, std::integral_constant<int, 2>{});
+      if constexpr (kPacked) issue_rope(1, std::integral_constant<int, 1>{});
       for (int s0 = 0; s0 <= stages; s0 += D) {
         step(s0, std::integral_constant<int, 0>{});
         if (s0 + 1 <= stages) step(s0 + 1, std::integral_constant<int, 1>{});
@@ -643,6 +691,10 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
         if (s0 + 3 <= stages) step(s0 + 3, std::integral_constant<int, 3>{});
       }
       wait_vm();  // drain the filler copies
+      if constexpr (kPacked) {  // the RoPE loads of the two stages past the end
+        wait_vm_regs<0>(rope_r[0][0], rope_r[0][1]);
+        wait_vm_regs<0>(rope_r[1][0], rope_r[1][1]);
+      }
       __syncthreads();  // consumers' maxima published
       float mtrue;
       const bool redo = redo_pass(mtrue);
