@@ -361,15 +361,29 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     if (kPacked) aux_tab[slot] = a.freqs ? (uint64_t)(a.freqs + (ok ? r : 0) * 4 * 64) : (uint64_t)a.q;
   };
   // the first kPcMaxChunk slots, read directly by all threads
+  constexpr int kEntries = (kPcMaxChunk + kPcThreads - 1) / kPcThreads;  // per thread
   auto build_table = [&]() {
-    for (int i = tid; i < kPcMaxChunk; i += kPcThreads) {
-      int64_t r = -1, pv = 0;
-      if (i < n) {
-        r = a.indices[t * a.topk + k0 + i];
-        if (paged && in_table(r)) pv = a.block_table[b * a.bt_stride + (r >> 6)];
-      }
-      put_entry(i, r, pv);
+    int64_t r[kEntries], pv[kEntries];
+#pragma unroll
+    for (int j = 0; j < kEntries; ++j) {  // top-k entries
+      const int i = tid + j * kPcThreads;
+      r[j] = -1;
+      pv[j] = 0;
+      if (i < kPcMaxChunk && i < n) r[j] = a.indices[t * a.topk + k0 + i];
     }
+    // then every block-table entry, by unconditional loads (Q's first word
+    // stands in where there is none): the compiler waits for a load made inside
+    // a branch before the next one, which would serialise a thread's entries
+#pragma unroll
+    for (int j = 0; j < kEntries; ++j) {
+      const bool has = paged && in_table(r[j]);
+      const int32_t* src = has ? a.block_table + (b * a.bt_stride + (r[j] >> 6)) : (const int32_t*)a.q;
+      const int32_t v = *src;
+      pv[j] = has ? v : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < kEntries; ++j)
+      if (tid + j * kPcThreads < kPcMaxChunk) put_entry(tid + j * kPcThreads, r[j], pv[j]);
   };
   build_table();
   wait_vm();
