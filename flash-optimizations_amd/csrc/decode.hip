@@ -709,6 +709,7 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
         wait_vm_regs<0>(rope_r[0][0], rope_r[0][1]);
         wait_vm_regs<0>(rope_r[1][0], rope_r[1][1]);
       }
+      if (stages <= 1) break;  // as the consumers: no second pass
       __syncthreads();  // consumers' maxima published
       float mtrue;
       const bool redo = redo_pass(mtrue);
@@ -825,6 +826,9 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    // a split of one stage took its reference from that stage: no overflow,
+    // and both roles skip the test's two barriers
+    if (stages <= 1) break;
     m_seen = fmaxf(m_seen, __shfl_xor(m_seen, 16, 64));
     m_seen = fmaxf(m_seen, __shfl_xor(m_seen, 32, 64));
     if (lane < 16) {
