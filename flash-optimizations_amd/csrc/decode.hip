@@ -446,6 +446,15 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     constexpr int D = G::kDepth;
     static_assert(D == 4, "the stage loop below is unrolled for a four-buffer ring");
     const int p = wv - kPcConsumers;
+    // Producers issue ahead of the consumers on the SIMDs they share (two of
+    // them hold a consumer and a producer each): the arbiter otherwise favours
+    // the older consumer waves, while the producers' expansion sets the stage
+    // time (interleaved runs: Packed B=64 33.2-33.8 -> 31.3-32.2 us, the
+    // reference H64/H128 shapes 0.2-1.5 us faster, Native and B=1 unchanged).
+    // Long splits keep equal priorities: their consumer wave 0 also refills
+    // the record table, and with the producers ahead B=128 x next-n 2 ran 8 %
+    // slower.
+    if constexpr (!kLong) __builtin_amdgcn_s_setprio(2);
     const uint8_t* const dummy = (const uint8_t*)a.q;
     // Copies of stage s into ring buffer B: the record table entries first,
     // then a fixed number of copies per stage. Invalid records and slots past
