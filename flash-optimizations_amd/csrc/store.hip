@@ -269,10 +269,10 @@ __device__ __forceinline__ uint32_t keep_at_threshold(const uint32_t* key, const
 // record's threshold exponent `hint` and its neighbours are tried with two or
 // three counts (consecutive records of a layer have thresholds within a
 // binade or two), then mantissa bits 22..16 come from a histogram of that
-// binade (FP32 keys: two more histogram levels and two bit-serial steps for
-// bits 15..0); when the exponent is
-// not among them the search runs bit-serially over all key bits. Both
-// ways give the same threshold. `at` is the count at the last accepted step,
+// binade (FP32 keys: up to two more histogram levels and two bit-serial
+// steps for bits 15..0, ending at the first level whose bin holds exactly the
+// keys still needed); when the exponent is not among them the search runs
+// bit-serially over all key bits. Both ways give the same keep set. `at` is the count at the last accepted step,
 // i.e. #{key >= threshold}; only when it exceeds kK is there a boundary tie to
 // admit in coordinate order.
 template <bool kBf16, int kK>
@@ -314,10 +314,18 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
       hint = te < 1 ? 1u : (te > 252 ? 252u : te);
       return keep_at_threshold<kK>(key, v, m, prefix, at, tied, ctab);
     }
+    // A level whose threshold bin holds exactly the keys still needed (at ==
+    // kK: the keys at or above the bin's start are the kK largest, the next
+    // key lies below the bin) ends the search: the finer levels would move
+    // the prefix up to the kK-th largest key and leave the same keep set.
     bin_histogram<kK, 16>(key, te << 23, above, hist, prefix, at, tied);
-    bin_histogram<kK, 9>(key, prefix, at - tied, hist, prefix, at, tied);
-    bin_histogram<kK, 2>(key, prefix, at - tied, hist, prefix, at, tied);
-    radix_bits<1, 0, kK>(key, prefix, at);
+    if (at != kK) {
+      bin_histogram<kK, 9>(key, prefix, at - tied, hist, prefix, at, tied);
+      if (at != kK) {
+        bin_histogram<kK, 2>(key, prefix, at - tied, hist, prefix, at, tied);
+        if (at != kK) radix_bits<1, 0, kK>(key, prefix, at);
+      }
+    }
   } else {
     prefix = 0;
     at = 512;
