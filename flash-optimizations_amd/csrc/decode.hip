@@ -31,7 +31,9 @@
 //     2^64 are far inside FP32/BF16 range; a split whose scores climb higher
 //     is recomputed once against its true max;
 //   * one workgroup barrier per stage hands the ring over: producers fill
-//     stage s while consumers read stage s - 1.
+//     stage s while consumers read stage s - 1. On splits of at most 512
+//     records the producers run at a higher wave priority than the consumers
+//     (two SIMDs hold one of each, and the producers set the stage time).
 // A Packed record (328 B, 8-byte aligned) is fetched as the 21 aligned 16-byte
 // pieces covering it: an even pool row from its start (its last piece reaches 8
 // bytes into the next row of the same page, which always exists because row 63
