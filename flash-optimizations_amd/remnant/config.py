@@ -251,11 +251,53 @@ def packed_profile() -> PackedProfile:
     return _current.profile
 
 
+LEGACY_FORMATS = ("native", "remnant")   # --dsv4-c4-cache-format (v0.5.18 pin)
+LEGACY_DECODE_IMPLS = ("kernel", "triton")
+STORE_IMPLS = ("triton", "kernel")
+
+
 def add_cli_arguments(parser: argparse.ArgumentParser) -> None:
-    parser.add_argument("--kv-cache-format", choices=FORMATS, default="native",
+    """Register the launcher's cache flags. scripts/local/run-server.sh:114-133
+    passes ``--kv-cache-format native|direct`` on the v0.5.22 pin or
+    ``--dsv4-c4-cache-format native|remnant --dsv4-c4-cache-implementation
+    kernel`` on v0.5.18, and on both pins the store implementation, the
+    default keep count and the per-layer counts when their environment
+    variables are set (STORE_IMPLEMENTATION, C4_KEEP_COUNT,
+    C4_LAYER_KEEP_COUNTS)."""
+    parser.add_argument("--kv-cache-format", choices=FORMATS, default=None,
                         help="native: 584-byte records; direct: Packed 328-byte records "
-                             "read by the Direct decode kernel")
+                             "read by the Direct decode kernel (default native)")
+    parser.add_argument("--dsv4-c4-cache-format", choices=LEGACY_FORMATS, default=None,
+                        help="v0.5.18 spelling of the format: remnant = Packed records")
+    parser.add_argument("--dsv4-c4-cache-implementation", choices=LEGACY_DECODE_IMPLS,
+                        default=None,
+                        help="Packed decode reader: kernel (Direct) or triton (reconstruct)")
+    parser.add_argument("--dsv4-c4-cache-store-implementation", choices=STORE_IMPLS,
+                        default=None, help="Packed store (one fused kernel serves both)")
+    parser.add_argument("--dsv4-c4-cache-keep-count", type=int, default=None,
+                        help="survivors per C4 record for every C4 layer (64..448, step 64)")
+    parser.add_argument("--dsv4-c4-cache-layer-keep-counts", default=None,
+                        help="per-layer overrides, 'layer:count' items separated by commas "
+                             "or spaces")
 
 
-def configure_from_args(args: argparse.Namespace) -> CacheFormat:
-    return configure_cache_format(args.kv_cache_format)
+def configure_from_args(args: argparse.Namespace, compression_ratios=None) -> CacheFormat:
+    """Resolve the launcher flags into one ``configure_cache_format`` call (the
+    same call serve.sh:178-183 makes from the same settings). The two format
+    spellings may both be given only when they agree. ``compression_ratios``
+    is the model's ``compress_ratios``, needed by per-layer counts. A rejected
+    profile raises ValueError before any pool exists and leaves the previous
+    configuration in place."""
+    fmt = getattr(args, "kv_cache_format", None)
+    legacy = getattr(args, "dsv4_c4_cache_format", None)
+    if fmt is not None and legacy is not None and \
+            ("remnant" if fmt == "direct" else fmt) != legacy:
+        raise ValueError(f"--kv-cache-format {fmt} contradicts --dsv4-c4-cache-format {legacy}")
+    fmt = fmt or legacy or "native"
+    keep = getattr(args, "dsv4_c4_cache_keep_count", None)
+    return configure_cache_format(
+        fmt, getattr(args, "dsv4_c4_cache_implementation", None) or "kernel",
+        getattr(args, "dsv4_c4_cache_store_implementation", None),
+        keep_count=KEEP_COUNT if keep is None else keep,
+        layer_keep_counts=getattr(args, "dsv4_c4_cache_layer_keep_counts", None),
+        compression_ratios=compression_ratios)

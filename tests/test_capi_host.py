@@ -212,6 +212,80 @@ def test_cache_format_configuration():
         remnant.configure_cache_format("native")
 
 
+def _launcher_args(pin, mode, env):
+    """The cache flags scripts/local/run-server.sh:114-133 appends for serving
+    mode ``mode`` (native|direct) on pin ``pin`` with environment ``env``."""
+    if pin == "v0.5.18":
+        args = ["--dsv4-c4-cache-format", "native" if mode == "native" else "remnant",
+                "--dsv4-c4-cache-implementation", "kernel"]
+    else:
+        args = ["--kv-cache-format", mode]
+    if env.get("STORE_IMPLEMENTATION"):
+        args += ["--dsv4-c4-cache-store-implementation", env["STORE_IMPLEMENTATION"]]
+    if env.get("C4_KEEP_COUNT"):
+        args += ["--dsv4-c4-cache-keep-count", env["C4_KEEP_COUNT"]]
+    if env.get("C4_LAYER_KEEP_COUNTS"):
+        args += ["--dsv4-c4-cache-layer-keep-counts", env["C4_LAYER_KEEP_COUNTS"]]
+    return args
+
+
+def test_launcher_flags_resolve_like_configure_cache_format():
+    """Every flag run-server.sh passes on either pin parses, and resolves to
+    the CacheFormat of the configure_cache_format call serve.sh:178-183 makes
+    from the same settings; rejected profiles fail before any pool exists."""
+    import argparse
+    ratios = (0, 128, 4, 128, 4, 0, 4)  # C4 layers 2, 4, 6
+    p = argparse.ArgumentParser()
+    config.add_cli_arguments(p)
+    p.add_argument("--tp", type=int)  # a server flag of its own, beside ours
+    envs = ({}, {"STORE_IMPLEMENTATION": "kernel"}, {"STORE_IMPLEMENTATION": "triton"},
+            {"C4_KEEP_COUNT": "256"}, {"C4_LAYER_KEEP_COUNTS": "2:256 6:256"},
+            {"STORE_IMPLEMENTATION": "kernel", "C4_KEEP_COUNT": "256",
+             "C4_LAYER_KEEP_COUNTS": "4=256,6:256"})
+    try:
+        for pin in ("v0.5.18", "v0.5.22"):
+            for mode in ("native", "direct"):
+                for env in envs:
+                    argv = ["--tp", "4"] + _launcher_args(pin, mode, env)
+                    got = config.configure_from_args(p.parse_args(argv), compression_ratios=ratios)
+                    want = remnant.configure_cache_format(
+                        "native" if mode == "native" else "remnant", "kernel",
+                        env.get("STORE_IMPLEMENTATION") or None,
+                        keep_count=int(env.get("C4_KEEP_COUNT") or 256),
+                        layer_keep_counts=env.get("C4_LAYER_KEEP_COUNTS") or None,
+                        compression_ratios=ratios)
+                    assert got == want, (pin, mode, env)
+                    assert got.packed == (mode == "direct")
+                    assert got.record_bytes == (328 if mode == "direct" else 584)
+        # the reconstruct reader through the v0.5.18 implementation flag
+        got = config.configure_from_args(p.parse_args(
+            ["--dsv4-c4-cache-format", "remnant", "--dsv4-c4-cache-implementation", "triton",
+             "--dsv4-c4-cache-keep-count", "192", "--dsv4-c4-cache-layer-keep-counts", "6:448"]),
+            compression_ratios=ratios)
+        assert got.decode_impl == "reconstruct" and got.profile.counts() == (192, 192, 448)
+        # no flag at all: Native
+        assert not config.configure_from_args(p.parse_args([])).packed
+        prev = config.current()
+        # rejected before any pool: non-256 with the Direct reader, counts that are
+        # no profile, overrides of non-C4 layers, contradicting format spellings
+        for argv in (_launcher_args("v0.5.22", "direct", {"C4_KEEP_COUNT": "192"}),
+                     _launcher_args("v0.5.18", "direct", {"C4_KEEP_COUNT": "192"}),
+                     _launcher_args("v0.5.18", "direct", {"C4_LAYER_KEEP_COUNTS": "4:128"}),
+                     _launcher_args("v0.5.22", "native", {"C4_KEEP_COUNT": "512"}),
+                     _launcher_args("v0.5.22", "direct", {"C4_LAYER_KEEP_COUNTS": "3:256"}),
+                     ["--kv-cache-format", "direct", "--dsv4-c4-cache-format", "native"]):
+            with pytest.raises(ValueError):
+                config.configure_from_args(p.parse_args(argv), compression_ratios=ratios)
+            assert config.current() == prev
+        for argv in (["--dsv4-c4-cache-format", "direct"],
+                     ["--dsv4-c4-cache-store-implementation", "cuda"],
+                     ["--dsv4-c4-cache-keep-count", "two"]):
+            with pytest.raises(SystemExit):
+                p.parse_args(argv)
+    finally:
+        remnant.configure_cache_format("native")
+
+
 def test_profiles_validate_counts_ids_and_atomic_updates():
     """Per-layer counts name C4 layers of the model (compress_ratios entry 4),
     in any of the launcher's spellings; a rejected call keeps the previous
