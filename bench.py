@@ -196,7 +196,8 @@ def build_decode(torch, remnant, contexts, q_len, topk, packed, seed, pool_pages
     c = dict(pool=pool, table=tab, idx=torch.from_numpy(idx).to(dev),
              lens=torch.from_numpy(lens).to(dev),
              seqlens=torch.tensor(contexts, dtype=torch.int32, device=dev), q=q, sink=sink,
-             freqs=freqs, packed=packed, valid=int(lens.sum()), swa=swa)
+             freqs=freqs, inv_freq=syn.rope_inv_freq().to(dev), packed=packed,
+             valid=int(lens.sum()), swa=swa)
     if swa:
         rows = len(contexts) * q_len * swa
         spool = remnant.LatentPool((rows + 63) // 64, fmt="native", device=dev)
@@ -208,8 +209,10 @@ def build_decode(torch, remnant, contexts, q_len, topk, packed, seed, pool_pages
     return c
 
 
-def time_decode(torch, remnant, c, reps=10, warm=5, samples=20):
-    """Median µs per decode call, from HIP-graph replays of `reps` calls."""
+def time_decode(torch, remnant, c, reps=10, warm=5, samples=20, rope="positions"):
+    """Median µs per decode call, from HIP-graph replays of `reps` calls.
+    Packed tails rotate by angles computed from the positions (rope
+    "positions") or by the table's rows ("table")."""
     tokens, heads = c["q"].shape[0] * c["q"].shape[1], c["q"].shape[2]
     _, need = remnant.get_decode_metadata(tokens, heads, c["idx"].shape[-1], c["swa"])
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
@@ -220,10 +223,13 @@ def time_decode(torch, remnant, c, reps=10, warm=5, samples=20):
     if c["swa"]:
         kw.update(swa_pool=c["swa_pool"], swa_indices=c["swa_idx"])
 
+    if c["packed"]:
+        kw.update({"rope_inv_freq": c["inv_freq"]} if rope == "positions"
+                  else {"freqs_cis": c["freqs"]})
+
     def call():
         if c["packed"]:
-            remnant.remnant_sparse_decode_fwd(c["q"], c["pool"], c["table"], c["idx"],
-                                              freqs_cis=c["freqs"], **kw)
+            remnant.remnant_sparse_decode_fwd(c["q"], c["pool"], c["table"], c["idx"], **kw)
         else:
             remnant.native_sparse_decode_fwd(c["q"], c["pool"], c["table"], c["idx"], **kw)
 
@@ -293,7 +299,11 @@ def decode_leg(torch, remnant, args):
                           "pool_bytes": c["pool"].nbytes(),
                           "records_resident": c["pool"].rows}
             if packed:
-                entry[key]["algorithmic_bytes_with_rope_table"] = decode_bytes(c, True)
+                entry[key]["rope"] = "positions"
+                us_t, _, _ = time_decode(torch, remnant, c, rope="table")
+                entry["direct_packed_rope_table"] = {
+                    "us_per_step": us_t, "algorithmic_bytes": decode_bytes(c, True),
+                    "GBps": decode_bytes(c, True) / (us_t * 1e3)}
             del c
             torch.cuda.empty_cache()
         entry["packed_over_native_time"] = entry["direct_packed"]["us_per_step"] / entry["native"]["us_per_step"]
@@ -334,6 +344,9 @@ def reference_shapes_leg(torch, remnant):
             c["valid"] = batch * valid
             us, _, _ = time_decode(torch, remnant, c)
             entry["direct_packed_us" if packed else "native_us"] = us
+            if packed:
+                entry["direct_packed_rope_table_us"] = time_decode(torch, remnant, c,
+                                                                   rope="table")[0]
             del c
             torch.cuda.empty_cache()
         entry["packed_over_native_time"] = entry["direct_packed_us"] / entry["native_us"]

@@ -14,14 +14,16 @@
 //     share is resolved once into LDS; invalid records and slots past the end
 //     point at a readable stand-in and are masked to zero;
 //   * four producer waves each own 8 records of every stage. They copy the
-//     record rows HBM -> LDS with global_load_lds three stages ahead (Packed:
-//     each lane loads the 32 bytes of RoPE row it rotates into registers two
-//     stages ahead, in the same in-order load stream) -- a fixed number of
-//     loads per stage, so their waits are compile-time vmcnt values -- and expand them into
-//     dense BF16 K rows in a four-slot LDS ring: v_perm places the kept E4M3
-//     codes (zeros for pruned coordinates) from a 256-entry selector table,
-//     v_cvt_scalef32_pk_bf16_fp8 applies the UE8M0 scale, the tail pairs are
-//     rotated (Packed) or copied as stored (Native);
+//     record rows HBM -> LDS with global_load_lds three stages ahead (Packed
+//     with a RoPE table: each lane also copies the 32 bytes of table row it
+//     rotates with, two stages ahead, in the same in-order load stream) -- a
+//     fixed number of loads per stage, so their waits are compile-time vmcnt
+//     values -- and expand them into dense BF16 K rows in a four-slot LDS
+//     ring: v_perm places the kept E4M3 codes (zeros for pruned coordinates)
+//     from a 256-entry selector table, v_cvt_scalef32_pk_bf16_fp8 applies the
+//     UE8M0 scale, the tail pairs are rotated (Packed: by the table row, or
+//     with inverse frequencies by the cos and sin of the angle from the
+//     record's position, computed in the lane) or copied as stored (Native);
 //   * two consumer waves each own 256 of the 512 output coordinates. Both
 //     compute S^T = K Q^T for every tile on v_mfma_f32_16x16x32_bf16 (Q in
 //     registers), take weights against a fixed per-head reference (the first
@@ -80,6 +82,7 @@ struct DecodeArgs {
   const float* sink;
   const float* freqs;
   int64_t freq_rows;
+  const float* inv_freq;   // position mode: [32] inverse frequencies (nullptr: identity)
   float scale_log2;
   int64_t q_len;
   int64_t heads;
@@ -135,22 +138,6 @@ __device__ __forceinline__ void dma4_opaque(const void* src, uint32_t lds) {
       : "=&s"(saved)
       : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds))
       : "memory");
-}
-// A 16-byte global load the compiler does not track: it adds no waits of its
-// own for it (the extra load in the in-order stream only lengthens the
-// compiler's other waits). The caller reads dst only through wait_vm_regs,
-// whose operands tie the registers to the wait, and reads every value it
-// loads that way, so no register is handed out again while a load into it is
-// in flight.
-__device__ __forceinline__ void load16_untracked(const void* src, f32x4& dst) {
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(dst) : "v"(src) : "memory");
-}
-// Wait until at most N global loads of this wave are outstanding; x and y are
-// read after the wait.
-template <int N>
-__device__ __forceinline__ void wait_vm_regs(f32x4& x, f32x4& y) {
-  static_assert(N >= 0 && N < 16, "vmcnt field");
-  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N) : "memory");
 }
 // This lane's index from instructions the compiler cannot hoist: values
 // derived from it are computed where they are used, not kept live across a
@@ -216,9 +203,6 @@ struct PcGeo {
   static constexpr int kCopies = (kPieceCount + 63) / 64;              // 16-B copies per stage
   static constexpr int kScaleAt = 1024 * kCopies;                      // Native: scale rows
   static constexpr int kBuf = kScaleAt + (kPacked ? 0 : 256);          // bytes per stage buffer
-  // global loads per stage: the copies, plus the Native scale row or the two
-  // Packed RoPE loads
-  static constexpr int kLoads = kCopies + (kPacked ? 2 : 1);
   static constexpr int kDepth = 4;  // copy ring buffers (the step loop is unrolled by 4)
 };
 
@@ -243,6 +227,9 @@ struct PcShared {
   int32_t idx_ring[3][64];
   int32_t bt_ring[3][64];
   uint64_t sel_tab[kPacked ? 256 : 1];
+  // table mode: per producer, a two-stage ring of the RoPE row bytes its
+  // lanes rotate with ([stage % 2][half][lane] 16 bytes)
+  alignas(16) uint8_t rope_ring[kPacked ? kPcProducers * 2 * 2 * 1024 : 1];
   float mrg[2 * kPcMaxGroups][2][16];  // consumers' (reference, seen) maxima per head
 };
 constexpr size_t kPcSmemBytes = sizeof(PcShared<true>) > sizeof(PcShared<false>)
@@ -261,11 +248,16 @@ __device__ __forceinline__ float max_over_rows(float x) {
 // One workgroup's share: split `split` of list `a` (a C4 top-k list through
 // the block table, or with a.block_table == nullptr a list of pool slots), for
 // kHG groups of 16 heads: every expanded record serves all of them.
-template <bool kPacked, int kHG, bool kPlanes = false, bool kLong = false>
+template <bool kPacked, int kHG, bool kPlanes = false, bool kLong = false, bool kPos = false>
 __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>* sm,
                                           const int split) {
   static_assert(kPacked || !kPlanes, "planes hold Packed records");
+  static_assert(kPacked || !kPos, "Native records store a rotated tail");
   using G = PcGeo<kPacked>;
+  // global loads per stage in a producer's in-order stream: the copies, plus
+  // the Native scale row or (table mode) the two Packed RoPE row loads
+  constexpr int kRopeLoads = kPacked && !kPos ? 2 : 0;
+  constexpr int kLoads = G::kCopies + (kPacked ? kRopeLoads : 1);
   constexpr int kPcConsumers = PcRoles<kHG>::kConsumers;
   constexpr int kPcThreads = PcRoles<kHG>::kThreads;
   auto& ktile = sm->ktile;
@@ -360,7 +352,11 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     row_tab[slot] = ok ? (uint64_t)(pg + (r & 63) * (kPlanes ? kCodeBytes : G::kData)) |
                              (kPacked ? 0 : (uint64_t)(r & 63) << 58)
                        : stand_in;
-    if (kPacked) aux_tab[slot] = a.freqs ? (uint64_t)(a.freqs + (ok ? r : 0) * 4 * 64) : (uint64_t)a.q;
+    // table mode: the record's RoPE row (row 0 of the table for an invalid
+    // record, Q without a table); position mode: the position 4 r as a float
+    // (0 for an invalid record, whose tail is zero)
+    if (kPacked && kPos) aux_tab[slot] = f2u(ok ? (float)(4 * r) : 0.0f);
+    else if (kPacked) aux_tab[slot] = a.freqs ? (uint64_t)(a.freqs + (ok ? r : 0) * 4 * 64) : (uint64_t)a.q;
   };
   // the first kPcMaxChunk slots, read directly by all threads
   constexpr int kEntries = (kPcMaxChunk + kPcThreads - 1) / kPcThreads;  // per thread
@@ -387,9 +383,17 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     for (int j = 0; j < kEntries; ++j)
       if (tid + j * kPcThreads < kPcMaxChunk) put_entry(tid + j * kPcThreads, r[j], pv[j]);
   };
+  // position mode: theta of the four RoPE pairs a producer lane rotates
+  // (lane / 8 = j: pairs 4 j .. 4 j + 3; zero, the identity, without inverse
+  // frequencies), loaded with the table and retired before the stage loop (the
+  // empty asm reads it once, so the compiler's own wait for it is not repeated
+  // inside the loop)
+  f32x4 theta = {0.f, 0.f, 0.f, 0.f};
+  if (kPos && a.inv_freq) theta = *(const f32x4*)(a.inv_freq + 4 * (lane >> 3));
   build_table();
   wait_vm();
   __syncthreads();
+  if constexpr (kPos) asm volatile("" : "+v"(theta));
 
   // Splits of more than kPcMaxChunk records: consumer 0 refills the table
   // ring ahead of the producers, after its MFMA work of each step s. It
@@ -581,24 +585,28 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
                   cvt2<true>(hi, gt.scale)};
       }
     };
-    // RoPE rows: lane (i, j) loads bytes 32 j .. 32 j + 31 of record i's row
-    // (the (cos, sin) of pairs 4j..4j+3) into a two-stage register ring, two
-    // stages ahead, after the stage's copies. For stages past the end it loads
-    // from Q (the loads per stage stay fixed).
-    f32x4 rope_r[2][2];
+    // Table mode: lane (i, j) copies bytes 32 j .. 32 j + 31 of record i's
+    // RoPE row (the (cos, sin) of pairs 4j..4j+3) HBM -> LDS into its own two
+    // 16-byte slots of a two-stage ring, two stages ahead, after the stage's
+    // copies. For stages past the end it copies from Q (the loads per stage
+    // stay fixed). Slot S is refilled at the step that rotated from it, after
+    // that rotation's reads returned. Position mode loads nothing: the lane
+    // holds theta of its four pairs and computes the angles.
+    auto rope_slot = [&](int S) { return &sm->rope_ring[(p * 2 + S) * 2 * 1024 + 16 * lane]; };
     auto issue_rope = [&](int s, auto slotc) {
       constexpr int S = decltype(slotc)::value;
       const uint64_t entry = aux_tab[(s * kPcStage + 8 * p + pi) & (kPcMaxChunk - 1)];
       const uint64_t row = s < stages ? entry : (uint64_t)a.q;
-      load16_untracked((const void*)(row + 32 * pw), rope_r[S][0]);
-      load16_untracked((const void*)(row + 32 * pw + 16), rope_r[S][1]);
+      const uint32_t base = lds_addr(&sm->rope_ring[(p * 2 + S) * 2 * 1024]);
+      dma16((const void*)(row + 32 * pw), base);
+      dma16((const void*)(row + 32 * pw + 16), base + 1024);
     };
-    // loads issued after the RoPE loads of stage s when stage s is rotated: the
-    // copies of stage s + 2, the RoPE loads of stage s + 1, the copies of s + 3
+    // loads issued after the RoPE copies of stage s when stage s is rotated: the
+    // copies of stage s + 2, the RoPE copies of stage s + 1, the copies of s + 3
     constexpr int kRopeLag = 2 * G::kCopies + 2;
-    auto rope_ready = [&](auto slotc) {
-      constexpr int S = decltype(slotc)::value;
-      wait_vm_regs<kRopeLag>(rope_r[S][0], rope_r[S][1]);
+    auto rope_ready = [&]() {
+      wait_vm_upto<kRopeLag>();
+      wave_lds_sync();
     };
     // tail: lane (i, j) rotates pairs 4j..4j+3 of record i (BF16 in, BF16 out);
     // an invalid record's tail is zero and its stand-in RoPE row finite; without
@@ -609,18 +617,29 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
       uint16_t* const tail = &ktile[(2 * s + (p >> 1)) % kPcRing][0] +
                              (8 * (p & 1) + pi) * kPcKPitch + kchunk(kNopeDim / 8 + pw);
       const u32x4 v = *(const u32x4*)tail;
-      rope_ready(std::integral_constant<int, B & 1>{});
-      const f32x4 f0 = rope_r[B & 1][0];
-      const f32x4 f1 = rope_r[B & 1][1];
+      float cs[8];
+      if constexpr (kPos) {  // angle RN(4 r * theta_j) of pairs 4 pw .. 4 pw + 3
+        const float pos = u2f((uint32_t)aux_tab[(s * kPcStage + 8 * p + pi) & (kPcMaxChunk - 1)]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rope_sincos(pos * theta[e], cs[2 * e + 1], cs[2 * e]);
+      } else {
+        rope_ready();
+        const uint8_t* slot = rope_slot(B & 1);
+        const f32x4 f0 = *(const f32x4*)slot;
+        const f32x4 f1 = *(const f32x4*)(slot + 1024);
+        const bool rope = a.freqs != nullptr;
+        const float t[8] = {rope ? f0[0] : 1.f, rope ? f0[1] : 0.f, rope ? f0[2] : 1.f,
+                            rope ? f0[3] : 0.f, rope ? f1[0] : 1.f, rope ? f1[1] : 0.f,
+                            rope ? f1[2] : 1.f, rope ? f1[3] : 0.f};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cs[e] = t[e];
+      }
       float x8[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         x8[2 * e] = u2f(v[e] << 16);
         x8[2 * e + 1] = u2f(v[e] & 0xffff0000u);
       }
-      const bool rope = a.freqs != nullptr;
-      float cs[8] = {rope ? f0[0] : 1.f, rope ? f0[1] : 0.f, rope ? f0[2] : 1.f, rope ? f0[3] : 0.f,
-                     rope ? f1[0] : 1.f, rope ? f1[1] : 0.f, rope ? f1[2] : 1.f, rope ? f1[3] : 0.f};
       rope4(x8, cs);
       const bf16x8 rot = {(__bf16)x8[0], (__bf16)x8[1], (__bf16)x8[2], (__bf16)x8[3],
                           (__bf16)x8[4], (__bf16)x8[5], (__bf16)x8[6], (__bf16)x8[7]};
@@ -675,7 +694,7 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
       // this wave's copies of stage s are done once at most the loads issued
       // after them remain outstanding: the later D - 2 stages' loads (Packed:
       // and the RoPE loads of stage s - 1, issued right after the copies)
-      wait_vm_upto<(D - 2) * G::kLoads + (kPacked ? 2 : 0)>();
+      wait_vm_upto<(D - 2) * kLoads + kRopeLoads>();
       wave_lds_sync();
       block_sync_lds();  // ring slots of stage s free (consumers are on stage s - 1)
       issue_stage(s + D - 1, std::integral_constant<int, (B + D - 1) % D>{});  // past the end: fillers
@@ -690,36 +709,30 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
         } else {
           produce_native(s, bufc);
         }
-      } else if constexpr (kPacked) {
-        rope_ready(std::integral_constant<int, B & 1>{});  // read, unused
       }
-      if constexpr (kPacked) issue_rope(s + 2, std::integral_constant<int, B & 1>{});
+      if constexpr (kPacked && !kPos) issue_rope(s + 2, std::integral_constant<int, B & 1>{});
     };
 
     for (int pass = 0; pass < 2; ++pass) {
       // the loads of steps -3 .. -1: copies of stages 0..2, each followed by
       // two RoPE loads (stage -1: two copies of Q into the idle ring buffer 3)
       issue_stage(0, std::integral_constant<int, 0>{});
-      if constexpr (kPacked) {
+      if constexpr (kPacked && !kPos) {
         const uint32_t idle = lds_addr(&raw[p][D - 1][0]);
         dma16(a.q, idle);
         dma16(a.q, idle + 1024);
       }
       issue_stage(1, std::integral_constant<int, 1>{});
-      if constexpr (kPacked) issue_rope(0, std::integral_constant<int, 0>{});
+      if constexpr (kPacked && !kPos) issue_rope(0, std::integral_constant<int, 0>{});
       issue_stage(2, std::integral_constant<int, 2>{});
-      if constexpr (kPacked) issue_rope(1, std::integral_constant<int, 1>{});
+      if constexpr (kPacked && !kPos) issue_rope(1, std::integral_constant<int, 1>{});
       for (int s0 = 0; s0 <= stages; s0 += D) {
         step(s0, std::integral_constant<int, 0>{});
         if (s0 + 1 <= stages) step(s0 + 1, std::integral_constant<int, 1>{});
         if (s0 + 2 <= stages) step(s0 + 2, std::integral_constant<int, 2>{});
         if (s0 + 3 <= stages) step(s0 + 3, std::integral_constant<int, 3>{});
       }
-      wait_vm();  // drain the filler copies
-      if constexpr (kPacked) {  // the RoPE loads of the two stages past the end
-        wait_vm_regs<0>(rope_r[0][0], rope_r[0][1]);
-        wait_vm_regs<0>(rope_r[1][0], rope_r[1][1]);
-      }
+      wait_vm();  // drain the filler copies (and the RoPE copies past the end)
       if (stages <= 1) break;  // as the consumers: no second pass
       __syncthreads();  // consumers' maxima published
       float mtrue;
@@ -902,11 +915,13 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
 }
 
 // kLong: splits may run past kPcMaxChunk records (the table ring refill),
-// compiled apart so that shorter splits carry none of its code.
-template <int kHG, bool kPlanes, bool kLong>
+// compiled apart so that shorter splits carry none of its code. kPos: the
+// RoPE rotation from positions and inverse frequencies instead of table rows.
+template <int kHG, bool kPlanes, bool kLong, bool kPos>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void packed_decode_pc_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[sizeof(PcShared<true>)];
-  decode_pc<true, kHG, kPlanes, kLong>(a, reinterpret_cast<PcShared<true>*>(smem), blockIdx.x);
+  decode_pc<true, kHG, kPlanes, kLong, kPos>(a, reinterpret_cast<PcShared<true>*>(smem),
+                                             blockIdx.x);
 }
 template <int kHG, bool kLong>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_decode_pc_kernel(DecodeArgs a) {
@@ -915,49 +930,61 @@ __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_decode_pc_kerne
 }
 // C4 list and window rows in one launch: workgroups x < c4.splits take a C4
 // split, the last column the window rows (Native records, one short split).
-template <bool kPacked, int kHG, bool kPlanes, bool kLong>
+template <bool kPacked, int kHG, bool kPlanes, bool kLong, bool kPos>
 __device__ __forceinline__ void decode_joint(const DecodeArgs& c4, const DecodeArgs& swa) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kPcSmemBytes];
   if ((int)blockIdx.x < c4.splits)
-    decode_pc<kPacked, kHG, kPlanes, kLong>(c4, reinterpret_cast<PcShared<kPacked>*>(smem),
-                                            blockIdx.x);
+    decode_pc<kPacked, kHG, kPlanes, kLong, kPos>(c4, reinterpret_cast<PcShared<kPacked>*>(smem),
+                                                  blockIdx.x);
   else
     decode_pc<false, kHG>(swa, reinterpret_cast<PcShared<false>*>(smem), 0);
 }
-template <int kHG, bool kPlanes, bool kLong>
+template <int kHG, bool kPlanes, bool kLong, bool kPos>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void packed_swa_decode_pc_kernel(
     DecodeArgs c4, DecodeArgs swa) {
-  decode_joint<true, kHG, kPlanes, kLong>(c4, swa);
+  decode_joint<true, kHG, kPlanes, kLong, kPos>(c4, swa);
 }
 template <int kHG, bool kLong>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_swa_decode_pc_kernel(
     DecodeArgs c4, DecodeArgs swa) {
-  decode_joint<false, kHG, false, kLong>(c4, swa);
+  decode_joint<false, kHG, false, kLong, false>(c4, swa);
 }
 
-// The workgroup kernel for a format, storage layout, head grouping and split length.
+// The workgroup kernel for a format, storage layout, head grouping, split
+// length and (Packed) RoPE source.
 using SplitKernel = void (*)(DecodeArgs);
 using JointKernel = void (*)(DecodeArgs, DecodeArgs);
-template <bool kPacked, bool kLong>
-SplitKernel split_kernel(bool planes, int hg) {
-  if constexpr (!kPacked)
-    return hg == 2 ? native_decode_pc_kernel<2, kLong> : native_decode_pc_kernel<1, kLong>;
-  else if (planes)
-    return hg == 2 ? packed_decode_pc_kernel<2, true, kLong> : packed_decode_pc_kernel<1, true, kLong>;
-  else
-    return hg == 2 ? packed_decode_pc_kernel<2, false, kLong>
-                   : packed_decode_pc_kernel<1, false, kLong>;
+template <bool kLong, bool kPos>
+SplitKernel packed_split_kernel(bool planes, int hg) {
+  if (planes)
+    return hg == 2 ? packed_decode_pc_kernel<2, true, kLong, kPos>
+                   : packed_decode_pc_kernel<1, true, kLong, kPos>;
+  return hg == 2 ? packed_decode_pc_kernel<2, false, kLong, kPos>
+                 : packed_decode_pc_kernel<1, false, kLong, kPos>;
 }
 template <bool kPacked, bool kLong>
-JointKernel joint_kernel(bool planes, int hg) {
+SplitKernel split_kernel(bool planes, int hg, bool pos) {
+  if constexpr (!kPacked)
+    return hg == 2 ? native_decode_pc_kernel<2, kLong> : native_decode_pc_kernel<1, kLong>;
+  else
+    return pos ? packed_split_kernel<kLong, true>(planes, hg)
+               : packed_split_kernel<kLong, false>(planes, hg);
+}
+template <bool kLong, bool kPos>
+JointKernel packed_joint_kernel(bool planes, int hg) {
+  if (planes)
+    return hg == 2 ? packed_swa_decode_pc_kernel<2, true, kLong, kPos>
+                   : packed_swa_decode_pc_kernel<1, true, kLong, kPos>;
+  return hg == 2 ? packed_swa_decode_pc_kernel<2, false, kLong, kPos>
+                 : packed_swa_decode_pc_kernel<1, false, kLong, kPos>;
+}
+template <bool kPacked, bool kLong>
+JointKernel joint_kernel(bool planes, int hg, bool pos) {
   if constexpr (!kPacked)
     return hg == 2 ? native_swa_decode_pc_kernel<2, kLong> : native_swa_decode_pc_kernel<1, kLong>;
-  else if (planes)
-    return hg == 2 ? packed_swa_decode_pc_kernel<2, true, kLong>
-                   : packed_swa_decode_pc_kernel<1, true, kLong>;
   else
-    return hg == 2 ? packed_swa_decode_pc_kernel<2, false, kLong>
-                   : packed_swa_decode_pc_kernel<1, false, kLong>;
+    return pos ? packed_joint_kernel<kLong, true>(planes, hg)
+               : packed_joint_kernel<kLong, false>(planes, hg);
 }
 
 // Butterfly over the wave's 64 lanes with the pairing of xor distances 1, 2,
@@ -1187,8 +1214,8 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
                   int64_t bt_stride, int64_t max_blocks, const int32_t* seqlens,
                   const int32_t* indices, int64_t topk, const int32_t* topk_length,
                   const Swa& w, const float* sink, const float* freqs, int64_t freq_rows,
-                  float scale, uint16_t* out, float* lse, void* workspace,
-                  size_t workspace_bytes, void* stream) {
+                  const float* inv_freq, float scale, uint16_t* out, float* lse,
+                  void* workspace, size_t workspace_bytes, void* stream) {
   const uint8_t* pool = src.pool;
   const int64_t pool_pages = src.pages;
   if (batch < 0 || q_len < 0 || topk < 0 || pool_pages < 0 || max_blocks < 0 || freq_rows < 0 ||
@@ -1210,6 +1237,7 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   if (topk > 0 && src.planes() && !src.scales) return RM_ERR_NULL;
   if (!aligned(q, 16) || !aligned(out, 16) || (pool && !aligned(pool, 16)) ||
       (w.pool && !aligned(w.pool, 16)) || (freqs && !aligned(freqs, 16)) ||
+      (inv_freq && !aligned(inv_freq, 16)) ||
       (src.planes() && !(aligned(src.bitmaps, 16) && aligned(src.scales, 16))))
     return RM_ERR_ALIGN;
   if (tokens > 65535) return RM_ERR_SHAPE;
@@ -1235,6 +1263,11 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   a.sink = sink;
   a.freqs = kPacked ? freqs : nullptr;
   a.freq_rows = freq_rows;
+  a.inv_freq = kPacked ? inv_freq : nullptr;
+  // Packed tails rotate from table rows only when a table and no inverse
+  // frequencies are given; otherwise by angles computed from the positions
+  // (theta = 0, the identity, with neither)
+  const bool pos = kPacked && (inv_freq || !freqs);
   a.scale_log2 = scale * kLog2e;
   a.q_len = q_len;
   a.heads = heads;
@@ -1266,17 +1299,18 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
     b.topk_length = w.length;
     b.freqs = nullptr;
     b.freq_rows = 0;
+    b.inv_freq = nullptr;
     b.chunk = kPcMaxChunk;
     b.splits = 1;
     b.ws_base = plan.splits;
     const dim3 grid((unsigned)slots, (unsigned)tokens, zblocks);
-    const JointKernel kern = lng ? joint_kernel<kPacked, true>(src.planes(), hg)
-                                 : joint_kernel<kPacked, false>(src.planes(), hg);
+    const JointKernel kern = lng ? joint_kernel<kPacked, true>(src.planes(), hg, pos)
+                                 : joint_kernel<kPacked, false>(src.planes(), hg, pos);
     hipLaunchKernelGGL(kern, grid, block, 0, s, a, b);
   } else {
     const dim3 grid((unsigned)plan.splits, (unsigned)tokens, zblocks);
-    const SplitKernel kern = lng ? split_kernel<kPacked, true>(src.planes(), hg)
-                                 : split_kernel<kPacked, false>(src.planes(), hg);
+    const SplitKernel kern = lng ? split_kernel<kPacked, true>(src.planes(), hg, pos)
+                                 : split_kernel<kPacked, false>(src.planes(), hg, pos);
     hipLaunchKernelGGL(kern, grid, block, 0, s, a);
   }
   if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
@@ -1320,12 +1354,12 @@ extern "C" int rm_remnant_sparse_decode_fwd(
     int64_t pool_pages, const int32_t* block_table, int64_t block_table_stride,
     int64_t max_blocks, const int32_t* seqlens, const int32_t* indices, int64_t topk,
     const int32_t* topk_length, const float* sink, const float* freqs, int64_t freq_rows,
-    float softmax_scale, uint16_t* out, float* lse, void* workspace, size_t workspace_bytes,
-    void* stream) {
+    const float* inv_freq, float softmax_scale, uint16_t* out, float* lse, void* workspace,
+    size_t workspace_bytes, void* stream) {
   return launch_decode<true>(q, batch, q_len, heads, paged(pool, pool_pages), block_table,
                              block_table_stride, max_blocks, seqlens, indices, topk, topk_length,
-                             Swa(), sink, freqs, freq_rows, softmax_scale, out, lse, workspace,
-                             workspace_bytes, stream);
+                             Swa(), sink, freqs, freq_rows, inv_freq, softmax_scale, out, lse,
+                             workspace, workspace_bytes, stream);
 }
 
 namespace {
@@ -1367,8 +1401,8 @@ extern "C" int rm_remnant_sparse_decode_swa_noalloc_fwd(
     int64_t max_blocks, const int32_t* seqlens, const int32_t* indices, int64_t topk,
     const int32_t* topk_length, const uint8_t* swa_pool, int64_t swa_pool_pages,
     const int32_t* swa_indices, int64_t swa_topk, const int32_t* swa_length, const float* sink,
-    const float* freqs, int64_t freq_rows, float softmax_scale, uint16_t* out, float* lse,
-    void* stream) {
+    const float* freqs, int64_t freq_rows, const float* inv_freq, float softmax_scale,
+    uint16_t* out, float* lse, void* stream) {
   // a partial slot set beyond the array is refused before any launch
   int32_t splits = 0;
   size_t need = 0;
@@ -1381,7 +1415,7 @@ extern "C" int rm_remnant_sparse_decode_swa_noalloc_fwd(
   return rm_remnant_sparse_decode_swa_fwd(q, batch, q_len, heads, pool, pool_pages, block_table,
                                           block_table_stride, max_blocks, seqlens, indices, topk,
                                           topk_length, swa_pool, swa_pool_pages, swa_indices,
-                                          swa_topk, swa_length, sink, freqs, freq_rows,
+                                          swa_topk, swa_length, sink, freqs, freq_rows, inv_freq,
                                           softmax_scale, out, lse, ws, need, stream);
 }
 
@@ -1391,8 +1425,8 @@ extern "C" int rm_remnant_sparse_decode_swa_fwd(
     int64_t max_blocks, const int32_t* seqlens, const int32_t* indices, int64_t topk,
     const int32_t* topk_length, const uint8_t* swa_pool, int64_t swa_pool_pages,
     const int32_t* swa_indices, int64_t swa_topk, const int32_t* swa_length, const float* sink,
-    const float* freqs, int64_t freq_rows, float softmax_scale, uint16_t* out, float* lse,
-    void* workspace, size_t workspace_bytes, void* stream) {
+    const float* freqs, int64_t freq_rows, const float* inv_freq, float softmax_scale,
+    uint16_t* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
   Swa w;
   w.pool = swa_pool;
   w.pool_pages = swa_pool_pages;
@@ -1401,8 +1435,8 @@ extern "C" int rm_remnant_sparse_decode_swa_fwd(
   w.length = swa_length;
   return launch_decode<true>(q, batch, q_len, heads, paged(pool, pool_pages), block_table,
                              block_table_stride, max_blocks, seqlens, indices, topk, topk_length,
-                             w, sink, freqs, freq_rows, softmax_scale, out, lse, workspace,
-                             workspace_bytes, stream);
+                             w, sink, freqs, freq_rows, inv_freq, softmax_scale, out, lse,
+                             workspace, workspace_bytes, stream);
 }
 
 extern "C" int rm_remnant_sparse_decode_planes_fwd(
@@ -1412,8 +1446,8 @@ extern "C" int rm_remnant_sparse_decode_planes_fwd(
     const int32_t* seqlens, const int32_t* indices, int64_t topk, const int32_t* topk_length,
     const uint8_t* swa_pool, int64_t swa_pool_pages, const int32_t* swa_indices,
     int64_t swa_topk, const int32_t* swa_length, const float* sink, const float* freqs,
-    int64_t freq_rows, float softmax_scale, uint16_t* out, float* lse, void* workspace,
-    size_t workspace_bytes, void* stream) {
+    int64_t freq_rows, const float* inv_freq, float softmax_scale, uint16_t* out, float* lse,
+    void* workspace, size_t workspace_bytes, void* stream) {
   if (pool_rows < 0 || pool_rows > ((int64_t)1 << 31)) return RM_ERR_SHAPE;
   if (!bitmaps && topk > 0) return RM_ERR_NULL;
   Src src;
@@ -1431,8 +1465,8 @@ extern "C" int rm_remnant_sparse_decode_planes_fwd(
   w.length = swa_length;
   return launch_decode<true>(q, batch, q_len, heads, src, block_table, block_table_stride,
                              max_blocks, seqlens, indices, topk, topk_length, w, sink, freqs,
-                             freq_rows, softmax_scale, out, lse, workspace, workspace_bytes,
-                             stream);
+                             freq_rows, inv_freq, softmax_scale, out, lse, workspace,
+                             workspace_bytes, stream);
 }
 
 extern "C" int rm_native_sparse_decode_fwd(
@@ -1443,8 +1477,8 @@ extern "C" int rm_native_sparse_decode_fwd(
     float* lse, void* workspace, size_t workspace_bytes, void* stream) {
   return launch_decode<false>(q, batch, q_len, heads, paged(pool, pool_pages), block_table,
                               block_table_stride, max_blocks, seqlens, indices, topk,
-                              topk_length, Swa(), sink, nullptr, 0, softmax_scale, out, lse,
-                              workspace, workspace_bytes, stream);
+                              topk_length, Swa(), sink, nullptr, 0, nullptr, softmax_scale, out,
+                              lse, workspace, workspace_bytes, stream);
 }
 
 extern "C" int rm_native_sparse_decode_swa_fwd(
@@ -1463,7 +1497,7 @@ extern "C" int rm_native_sparse_decode_swa_fwd(
   w.length = swa_length;
   return launch_decode<false>(q, batch, q_len, heads, paged(pool, pool_pages), block_table,
                               block_table_stride, max_blocks, seqlens, indices, topk,
-                              topk_length, w, sink, nullptr, 0, softmax_scale, out, lse,
+                              topk_length, w, sink, nullptr, 0, nullptr, softmax_scale, out, lse,
                               workspace, workspace_bytes, stream);
 }
 

@@ -160,6 +160,25 @@ __device__ __forceinline__ float inv_rms(float sumsq, float eps) {
   return inv_root(__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x))));
 }
 
+// cos and sin of a RoPE angle x = RN(pos * theta), for |x| < 2^24. The angle
+// is first taken in revolutions, x / (2 pi), with 1 / (2 pi) split into a
+// float kI1 = RN(1 / (2 pi)) and the remainder kI2 = RN(1 / (2 pi) - kI1): the
+// product x * kI1 and its exact rounding error (one FMA) plus x * kI2 give the
+// fractional revolutions f in [-1/2, 1/2] to about 2^-28 for |x| < 2^24 (the
+// subtraction of the nearest integer is exact below 2^23 revolutions). The
+// hardware v_sin_f32 / v_cos_f32, whose argument is in revolutions, then
+// evaluate sin(2 pi f) and cos(2 pi f).
+__device__ __forceinline__ void rope_sincos(float x, float& s, float& c) {
+  constexpr float kI1 = 0x1.45f306p-3f;
+  constexpr float kI2 = 0x1.b93910p-28f;
+  const float ph = x * kI1;
+  float pl = __builtin_fmaf(x, kI1, -ph);
+  pl = __builtin_fmaf(x, kI2, pl);
+  const float f = (ph - __builtin_rintf(ph)) + pl;
+  s = __builtin_amdgcn_sinf(f);
+  c = __builtin_amdgcn_cosf(f);
+}
+
 // Tail rotation of 4 interleaved (re, im) pairs held as floats, with
 // (cos, sin) pairs from the frequency table: re' = xr*c - xi*s, im' = xr*s + xi*c,
 // every product rounded (compiled without FMA contraction).

@@ -128,6 +128,45 @@ __global__ __launch_bounds__(kThreads) void bf16_array_kernel(const float* x, ui
     out[i] = __builtin_bit_cast(uint32_t, bf16_pair(x[2 * i], x[2 * i + 1]));
 }
 
+// RoPE rotation of the Direct decode's position mode: out[2 (p * 32 + j)] and
+// out[2 (p * 32 + j) + 1] = cos and sin of RN(pos * theta[j]), pos = p * step.
+__global__ __launch_bounds__(kThreads) void rope_cs_kernel(const float* theta, int64_t n_pos,
+                                                           int step, float* out) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_pos * kRopePairs;
+       i += (int64_t)gridDim.x * kThreads) {
+    const int64_t p = i / kRopePairs;
+    const float x = (float)(p * step) * theta[i - p * kRopePairs];
+    float s, c;
+    rope_sincos(x, s, c);
+    out[2 * i] = c;
+    out[2 * i + 1] = s;
+  }
+}
+
+// Largest |v_sin_f32(f) - sin(2 pi f)| and |v_cos_f32(f) - cos(2 pi f)| (in
+// double) over the FP32 bit patterns [first, end) of one sign: err[0] and
+// err[1] as float bit patterns (non-negative floats order as integers).
+__global__ __launch_bounds__(kThreads) void sincos_error_kernel(uint32_t first, uint32_t end,
+                                                                unsigned int* err) {
+  float es = 0.0f, ec = 0.0f;
+  for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; first + i < end;
+       i += (uint64_t)gridDim.x * kThreads) {
+    const float f = u2f(first + (uint32_t)i);
+    const double a = (double)f * 6.283185307179586476925286766559;
+    es = fmaxf(es, (float)fabs((double)__builtin_amdgcn_sinf(f) - sin(a)));
+    ec = fmaxf(ec, (float)fabs((double)__builtin_amdgcn_cosf(f) - cos(a)));
+  }
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    es = fmaxf(es, __shfl_xor(es, d, 64));
+    ec = fmaxf(ec, __shfl_xor(ec, d, 64));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicMax(err, f2u(es));
+    atomicMax(err + 1, f2u(ec));
+  }
+}
+
 int status() { return hipGetLastError() == hipSuccess ? 0 : -6; }
 
 }  // namespace
@@ -179,5 +218,23 @@ extern "C" int rmt_bf16_array(const float* x, uint16_t* out, int64_t n, void* st
   if (n == 0) return 0;
   hipLaunchKernelGGL(bf16_array_kernel, dim3(kBlocks), dim3(kThreads), 0, (hipStream_t)stream, x,
                      (uint32_t*)out, n / 2);
+  return status();
+}
+
+// out: device [n_pos * 32 * 2] f32; theta: device [32] f32.
+extern "C" int rmt_rope_cos_sin(const float* theta, int64_t n_pos, int step, float* out,
+                                void* stream) {
+  if (n_pos < 0 || step < 0 || (double)n_pos * step >= 16777216.0) return -2;
+  if (n_pos == 0) return 0;
+  hipLaunchKernelGGL(rope_cs_kernel, dim3(kBlocks), dim3(kThreads), 0, (hipStream_t)stream, theta,
+                     n_pos, step, out);
+  return status();
+}
+
+// err: device [2] u32, zeroed by the caller.
+extern "C" int rmt_sincos_error(uint32_t first, uint32_t end, unsigned int* err, void* stream) {
+  if (end < first) return -2;
+  hipLaunchKernelGGL(sincos_error_kernel, dim3(kBlocks), dim3(kThreads), 0, (hipStream_t)stream,
+                     first, end, err);
   return status();
 }

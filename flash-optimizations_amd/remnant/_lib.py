@@ -41,8 +41,8 @@ SIGNATURES = {
                                           _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "rm_remnant_sparse_decode_planes_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64,
                                                    _vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp,
-                                                   _i64, _vp, _i64, _vp, _vp, _vp, _i64, _f32,
-                                                   _vp, _vp, _vp, _sz, _vp]),
+                                                   _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp,
+                                                   _f32, _vp, _vp, _vp, _sz, _vp]),
     "rm_unpack_gather_bf16": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
                                      _i64, _i64, _vp, _i64, _vp, _vp]),
     "rm_unpack_gather_bf16_k": (_i32, [_vp, _i64, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp,
@@ -54,8 +54,8 @@ SIGNATURES = {
     "rm_sparse_decode_workspace": (_i32, [_i64, _i64, _i64, ctypes.POINTER(ctypes.c_int32),
                                           ctypes.POINTER(ctypes.c_size_t)]),
     "rm_remnant_sparse_decode_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64,
-                                            _vp, _vp, _i64, _vp, _vp, _vp, _i64, _f32, _vp, _vp,
-                                            _vp, _sz, _vp]),
+                                            _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _f32, _vp,
+                                            _vp, _vp, _sz, _vp]),
     "rm_native_sparse_decode_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64,
                                            _vp, _vp, _i64, _vp, _vp, _f32, _vp, _vp, _vp, _sz,
                                            _vp]),
@@ -64,12 +64,12 @@ SIGNATURES = {
                                               ctypes.POINTER(ctypes.c_size_t)]),
     "rm_remnant_sparse_decode_swa_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
                                                 _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64,
-                                                _vp, _vp, _vp, _i64, _f32, _vp, _vp, _vp, _sz,
-                                                _vp]),
+                                                _vp, _vp, _vp, _i64, _vp, _f32, _vp, _vp, _vp,
+                                                _sz, _vp]),
     "rm_remnant_sparse_decode_swa_noalloc_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp,
                                                         _i64, _i64, _vp, _vp, _i64, _vp, _vp,
                                                         _i64, _vp, _i64, _vp, _vp, _vp, _i64,
-                                                        _f32, _vp, _vp, _vp]),
+                                                        _vp, _f32, _vp, _vp, _vp]),
     "rm_native_sparse_decode_swa_fwd": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
                                                _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64,
                                                _vp, _vp, _f32, _vp, _vp, _vp, _sz, _vp]),

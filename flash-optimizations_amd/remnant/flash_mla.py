@@ -82,7 +82,7 @@ def remnant_buffers(values, bitmaps=None, scales=None, *, layer_id=None) -> Remn
 
 def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length, sink,
             freqs_cis, softmax_scale, out, lse, workspace, layer_id, swa_pool=None,
-            swa_indices=None, swa_lengths=None):
+            swa_indices=None, swa_lengths=None, rope_inv_freq=None):
     src, is_packed, keep = _as_source(pool, layer_id)
     buf = src if not is_packed else None
     if is_packed != packed:
@@ -120,6 +120,15 @@ def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length
         freq_ptr, freq_rows = freqs_cis.data_ptr(), freqs_cis.numel() // (config.ROPE_DIM // 2)
         if freq_rows == 0:
             raise ValueError("freqs_cis must hold at least one row of 32 frequencies")
+    inv_ptr = None
+    if rope_inv_freq is not None:
+        if not packed:
+            raise ValueError("Native records store a rotated tail; rope_inv_freq is not used")
+        if rope_inv_freq.dtype != torch.float32 or rope_inv_freq.numel() != config.ROPE_DIM // 2 \
+                or not rope_inv_freq.is_contiguous():
+            raise ValueError("rope_inv_freq must be a contiguous float32 tensor of 32 inverse "
+                             "frequencies")
+        inv_ptr = rope_inv_freq.data_ptr()
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(config.HEAD_DIM)
     if out is None:
@@ -144,7 +153,7 @@ def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length
         raise ValueError("plane buffers need an even number of rows")
     pool_tensors = src.tensors() if packed else (buf,)
     _check_cuda(q, *pool_tensors, block_table, indices, seqlens, topk_length, sink, freqs_cis,
-                out, lse, sbuf, sidx, slen, workspace)
+                rope_inv_freq, out, lse, sbuf, sidx, slen, workspace)
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     ws_ptr = ptr(workspace) if need else None
     ws_bytes = workspace.numel() * workspace.element_size() if need else 0
@@ -155,8 +164,8 @@ def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length
             src.scales.data_ptr(), src.rows, block_table.data_ptr(), bt_stride,
             block_table.shape[1], ptr(seqlens), indices.data_ptr(), topk, ptr(topk_length),
             ptr(sbuf), 0 if sbuf is None else sbuf.shape[0], ptr(sidx), width, ptr(slen),
-            ptr(sink), freq_ptr, freq_rows, float(softmax_scale), out.data_ptr(), lse.data_ptr(),
-            ws_ptr, ws_bytes, _stream()), "rm_remnant_sparse_decode_planes_fwd")
+            ptr(sink), freq_ptr, freq_rows, inv_ptr, float(softmax_scale), out.data_ptr(),
+            lse.data_ptr(), ws_ptr, ws_bytes, _stream()), "rm_remnant_sparse_decode_planes_fwd")
         return out, lse
     if packed:
         buf = src.pages
@@ -167,7 +176,8 @@ def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length
                   sidx.data_ptr(), width, ptr(slen), ptr(sink))
         tail = (float(softmax_scale), out.data_ptr(), lse.data_ptr(), ws_ptr, ws_bytes, _stream())
         if packed:
-            _lib.check(lib.rm_remnant_sparse_decode_swa_fwd(*common, freq_ptr, freq_rows, *tail),
+            _lib.check(lib.rm_remnant_sparse_decode_swa_fwd(*common, freq_ptr, freq_rows, inv_ptr,
+                                                            *tail),
                        "rm_remnant_sparse_decode_swa_fwd")
         else:
             _lib.check(lib.rm_native_sparse_decode_swa_fwd(*common, *tail),
@@ -176,7 +186,7 @@ def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length
         status = lib.rm_remnant_sparse_decode_fwd(
             q.data_ptr(), batch, q_len, heads, buf.data_ptr(), buf.shape[0],
             block_table.data_ptr(), bt_stride, block_table.shape[1], ptr(seqlens),
-            indices.data_ptr(), topk, ptr(topk_length), ptr(sink), freq_ptr, freq_rows,
+            indices.data_ptr(), topk, ptr(topk_length), ptr(sink), freq_ptr, freq_rows, inv_ptr,
             float(softmax_scale), out.data_ptr(), lse.data_ptr(), ws_ptr, ws_bytes, _stream())
         _lib.check(status, "rm_remnant_sparse_decode_fwd")
     else:
@@ -192,14 +202,21 @@ def _decode(packed: bool, q, pool, block_table, indices, *, seqlens, topk_length
 def remnant_sparse_decode_fwd(q, pool, block_table, indices, *, seqlens=None, topk_length=None,
                               sink=None, freqs_cis=None, softmax_scale=None, out=None, lse=None,
                               workspace=None, layer_id=None, swa_pool=None, swa_indices=None,
-                              swa_lengths=None):
+                              swa_lengths=None, rope_inv_freq=None):
     """Direct packed sparse-MLA decode (with the window rows when ``swa_pool``
-    is given). Returns (out [B, Sq, H, 512] bf16, lse [B, Sq, H])."""
+    is given). Returns (out [B, Sq, H, 512] bf16, lse [B, Sq, H]).
+
+    The stored pre-RoPE tail of logical record r is rotated by row 4 r of
+    ``freqs_cis`` (complex64 [P, 32]; a record with 4 r >= P contributes
+    nothing). With ``rope_inv_freq`` (float32 [32], the theta_j the table is
+    built from as ``polar(1, outer(positions, theta))``) the kernel computes
+    those rotations from the positions instead of reading 256-byte table rows
+    (within a few FP32 ulps of the table); ``freqs_cis`` may then be omitted."""
     return _decode(True, q, pool, block_table, indices, seqlens=seqlens,
                    topk_length=topk_length, sink=sink, freqs_cis=freqs_cis,
                    softmax_scale=softmax_scale, out=out, lse=lse, workspace=workspace,
                    layer_id=layer_id, swa_pool=swa_pool, swa_indices=swa_indices,
-                   swa_lengths=swa_lengths)
+                   swa_lengths=swa_lengths, rope_inv_freq=rope_inv_freq)
 
 
 def native_sparse_decode_fwd(q, pool, block_table, indices, *, seqlens=None, topk_length=None,
@@ -218,4 +235,5 @@ def sparse_decode_fwd(q, pool, block_table, indices, **kwargs):
     if config.current().packed:
         return remnant_sparse_decode_fwd(q, pool, block_table, indices, **kwargs)
     kwargs.pop("freqs_cis", None)
+    kwargs.pop("rope_inv_freq", None)
     return native_sparse_decode_fwd(q, pool, block_table, indices, **kwargs)

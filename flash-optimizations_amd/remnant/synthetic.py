@@ -25,10 +25,14 @@ def latents(rows: int, seed: int = SEED, dtype=torch.bfloat16) -> torch.Tensor:
     return x.to(dtype)
 
 
+def rope_inv_freq() -> torch.Tensor:
+    """float32 [32]: theta_j = 10000^(-j/32), the inverse frequencies of the table."""
+    return 1.0 / (10000.0 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))
+
+
 def rope_freqs(positions: int) -> torch.Tensor:
-    """complex64 [positions, 32]."""
-    inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))
-    ang = torch.outer(torch.arange(positions, dtype=torch.float32), inv)
+    """complex64 [positions, 32]: polar(1, pos * theta_j) with the angle in float32."""
+    ang = torch.outer(torch.arange(positions, dtype=torch.float32), rope_inv_freq())
     return torch.polar(torch.ones_like(ang), ang)
 
 

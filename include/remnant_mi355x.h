@@ -226,7 +226,14 @@ int rm_sparse_decode_workspace(int64_t tokens, int64_t heads, int64_t topk,
  * records (-1 = padding), topk <= 32768. topk_length: [batch * q_len] int32
  * (NULL = topk).
  * sink: [heads] f32 logits (NULL = no sink). freqs/freq_rows: RoPE table for
- * the stored pre-RoPE tail, row = record * 4 (NULL = tail used as stored).
+ * the stored pre-RoPE tail, row = record * 4, complex64 rows of 32 (cos, sin)
+ * pairs; a record whose row r * 4 >= freq_rows contributes nothing.
+ * inv_freq: [32] f32 inverse frequencies theta_j, 16-byte aligned (NULL = none).
+ * With inv_freq the tail of record r is rotated by the angles RN(RN(4 r) *
+ * theta_j), their cos and sin evaluated in the kernel (within a few FP32 ulps
+ * of the row 4 r of a table built as polar(1, pos * theta)), and no table row
+ * is read; freqs may then be NULL, and when given still bounds the valid
+ * records. Neither table nor inv_freq: the tail is used as stored.
  * Output: out [batch * q_len, heads, 512] BF16; lse [batch * q_len, heads] f32,
  * natural log of sum_j exp(l_j) + exp(sink). Invalid entries (k >= length,
  * r < 0, r >= seqlen, unmapped block, row beyond the table) contribute nothing.
@@ -237,9 +244,9 @@ int rm_remnant_sparse_decode_fwd(const uint16_t* q, int64_t batch, int64_t q_len
                                  int64_t max_blocks, const int32_t* seqlens,
                                  const int32_t* indices, int64_t topk,
                                  const int32_t* topk_length, const float* sink,
-                                 const float* freqs, int64_t freq_rows, float softmax_scale,
-                                 uint16_t* out, float* lse, void* workspace,
-                                 size_t workspace_bytes, void* stream);
+                                 const float* freqs, int64_t freq_rows, const float* inv_freq,
+                                 float softmax_scale, uint16_t* out, float* lse,
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* rm_remnant_sparse_decode_swa_fwd on plane-form buffers of pool_rows
  * 256-survivor records (values [rows, 256], bitmaps [rows, 8], scales [rows, 8];
@@ -253,8 +260,8 @@ int rm_remnant_sparse_decode_planes_fwd(
     const int32_t* seqlens, const int32_t* indices, int64_t topk, const int32_t* topk_length,
     const uint8_t* swa_pool, int64_t swa_pool_pages, const int32_t* swa_indices,
     int64_t swa_topk, const int32_t* swa_length, const float* sink, const float* freqs,
-    int64_t freq_rows, float softmax_scale, uint16_t* out, float* lse, void* workspace,
-    size_t workspace_bytes, void* stream);
+    int64_t freq_rows, const float* inv_freq, float softmax_scale, uint16_t* out, float* lse,
+    void* workspace, size_t workspace_bytes, void* stream);
 
 /* rm_remnant_sparse_decode_swa_fwd without a workspace argument: the split
  * partials live in a 32 MiB device array inside the library (one per GPU,
@@ -270,8 +277,8 @@ int rm_remnant_sparse_decode_swa_noalloc_fwd(
     int64_t max_blocks, const int32_t* seqlens, const int32_t* indices, int64_t topk,
     const int32_t* topk_length, const uint8_t* swa_pool, int64_t swa_pool_pages,
     const int32_t* swa_indices, int64_t swa_topk, const int32_t* swa_length, const float* sink,
-    const float* freqs, int64_t freq_rows, float softmax_scale, uint16_t* out, float* lse,
-    void* stream);
+    const float* freqs, int64_t freq_rows, const float* inv_freq, float softmax_scale,
+    uint16_t* out, float* lse, void* stream);
 
 /* Native control decode: same contract on 584-byte records (tail already rotated). */
 int rm_native_sparse_decode_fwd(const uint16_t* q, int64_t batch, int64_t q_len,
@@ -307,8 +314,9 @@ int rm_remnant_sparse_decode_swa_fwd(const uint16_t* q, int64_t batch, int64_t q
                                      int64_t swa_pool_pages, const int32_t* swa_indices,
                                      int64_t swa_topk, const int32_t* swa_length,
                                      const float* sink, const float* freqs, int64_t freq_rows,
-                                     float softmax_scale, uint16_t* out, float* lse,
-                                     void* workspace, size_t workspace_bytes, void* stream);
+                                     const float* inv_freq, float softmax_scale, uint16_t* out,
+                                     float* lse, void* workspace, size_t workspace_bytes,
+                                     void* stream);
 
 /* Native control decode with the sliding window (same contract, 584-byte C4 records). */
 int rm_native_sparse_decode_swa_fwd(const uint16_t* q, int64_t batch, int64_t q_len,

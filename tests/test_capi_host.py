@@ -78,8 +78,8 @@ def test_capi_rejects_bad_arguments_without_launching():
     assert lib.rm_pack_rows_k(None, 1, 512, w, 1e-6, s, 4, pool, 1, 64, None) == -1
     assert lib.rm_unpack_gather_bf16_k(pool, 1, 192, s, 1, 1, None, 0, 0, s, 1, 0, 5, None, 0,
                                        x, None) == 0
-    args = [x, 1, 1, 17, pool, 1, s, 4, 4, None, s, 8, None, None, None, 0, 0.1, x, w, None, 0,
-            None]
+    args = [x, 1, 1, 17, pool, 1, s, 4, 4, None, s, 8, None, None, None, 0, None, 0.1, x, w,
+            None, 0, None]
     assert lib.rm_remnant_sparse_decode_fwd(*args) == -2  # 17 heads
     args[3] = 16
     args[8] = 9  # max_blocks beyond the table stride
@@ -91,6 +91,10 @@ def test_capi_rejects_bad_arguments_without_launching():
                                            None, 0.1, x, w, None, 0, None) == 0
     args[11] = 32769  # top-k beyond 64 splits of 512 records
     assert lib.rm_remnant_sparse_decode_fwd(*args) == -2
+    args[11] = 8
+    args[16] = w + 4  # inverse frequencies not 16-byte aligned
+    assert lib.rm_remnant_sparse_decode_fwd(*args) == -3
+    args[16] = None
     splits, nbytes = ctypes.c_int32(), ctypes.c_size_t()
     assert lib.rm_sparse_decode_workspace(1, 16, 32769, ctypes.byref(splits),
                                           ctypes.byref(nbytes)) == -2
@@ -107,7 +111,7 @@ def test_capi_rejects_bad_arguments_without_launching():
                                               ctypes.byref(nbytes)) == 0
     assert splits.value == 2 and nbytes.value == 300 * 2 * 16 * 513 * 4
     swa_args = [x, 1, 1, 16, pool, 1, s, 4, 4, None, s, 8, None, None, 0, s, 8, None, None,
-                None, 0, 0.1, x, w, None, 0, None]
+                None, 0, None, 0.1, x, w, None, 0, None]
     assert lib.rm_remnant_sparse_decode_swa_fwd(*swa_args) == -1  # window slots without a pool
     swa_args[13], swa_args[14] = pool + 8, 1
     assert lib.rm_remnant_sparse_decode_swa_fwd(*swa_args) == -3  # unaligned window pool
@@ -459,7 +463,7 @@ def test_native_store_and_decode_argument_checks():
     _, s = buf(64)
     _, f = buf(256)
     assert lib.rm_remnant_sparse_decode_fwd(xq, 1, 1, 16, pg, 1, s, 4, 4, None, s, 8, None,
-                                            None, f, 0, 0.1, xq, f, None, 0, None) == -2
+                                            None, f, 0, None, 0.1, xq, f, None, 0, None) == -2
 
 
 def test_adapter_host_validation():
@@ -663,7 +667,7 @@ def test_plane_buffer_validation_and_remnant_buffers():
     assert lib.rm_pack_rows_planes(xq, 1, 512, f, 1e-6, ix, 1, vp + 4, bp, sp, 4, 256,
                                    None) == -3
     dec = [xq, 1, 1, 16, vp, bp, sp, 5, ix, 4, 4, None, ix, 4, None, None, 0, None, 0, None,
-           None, None, 0, 0.1, out, f, None, 0, None]
+           None, None, 0, None, 0.1, out, f, None, 0, None]
     assert lib.rm_remnant_sparse_decode_planes_fwd(*dec) == -2  # odd rows
     dec[7] = 4
     dec[5] = bp + 8

@@ -181,12 +181,14 @@ def test_extreme_bitmaps_pack_reconstruct_and_decode():
 
 # ---- graph replay with changing inputs --------------------------------------------------------
 
+@pytest.mark.parametrize("rope", ["table", "positions"])
 @pytest.mark.parametrize("batch,heads,topk", [(8, 64, 64), (1, 16, 2048)])
-def test_direct_decode_graph_replay_with_changed_inputs(batch, heads, topk):
+def test_direct_decode_graph_replay_with_changed_inputs(batch, heads, topk, rope):
     """The decode (and its split combine) captured once; q, indices, lengths
     and the records change in place between replays; every replay equals an
-    eager call bit for bit and the oracle within tolerance."""
-    banner(f"decode graph replay B={batch} H={heads} topk={topk}")
+    eager call bit for bit and the oracle within tolerance. The tail rotation
+    comes from the table rows or (positions) from the inverse frequencies."""
+    banner(f"decode graph replay B={batch} H={heads} topk={topk} rope={rope}")
     rng = np.random.default_rng(420 + batch)
     contexts = [int(v) for v in rng.integers(max(topk, 200), 4 * topk + 300, batch)]
     c = build_decode_case(contexts, q_len=1, heads=heads, topk=topk, seed=421 + batch)
@@ -197,7 +199,8 @@ def test_direct_decode_graph_replay_with_changed_inputs(batch, heads, topk):
     lens = torch.from_numpy(c["lens"]).to(DEV)
     seq = torch.tensor(contexts, dtype=torch.int32, device=DEV)
     sink = c["sink"].to(DEV)
-    freqs = c["freqs"].to(DEV)
+    rope_kw = ({"rope_inv_freq": syn.rope_inv_freq().to(DEV)} if rope == "positions"
+               else {"freqs_cis": c["freqs"].to(DEV)})
     _, need = remnant.get_decode_metadata(tokens, heads, topk)
     ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=DEV)
     out = torch.empty_like(q)
@@ -207,7 +210,7 @@ def test_direct_decode_graph_replay_with_changed_inputs(batch, heads, topk):
 
     def call(o, l):
         remnant.remnant_sparse_decode_fwd(q, c["pool"], bt, idx, seqlens=seq, topk_length=lens,
-                                          sink=sink, freqs_cis=freqs, out=o, lse=l, workspace=ws)
+                                          sink=sink, out=o, lse=l, workspace=ws, **rope_kw)
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())

@@ -589,8 +589,13 @@ def run_decode(c):
     bt = torch.from_numpy(c["table"]).to(DEV)
     idx = torch.from_numpy(c["idx"]).to(DEV)
     if c["packed"]:
-        out, lse = remnant.remnant_sparse_decode_fwd(q, c["pool"], bt, idx,
-                                                     freqs_cis=c["freqs"].to(DEV), **kw)
+        # RoPE from the table rows, or (c["rope"] == "positions") from the
+        # positions and the table's inverse frequencies, computed in the kernel
+        if c.get("rope") == "positions":
+            kw["rope_inv_freq"] = syn.rope_inv_freq().to(DEV)
+        else:
+            kw["freqs_cis"] = c["freqs"].to(DEV)
+        out, lse = remnant.remnant_sparse_decode_fwd(q, c["pool"], bt, idx, **kw)
     else:
         out, lse = remnant.native_sparse_decode_fwd(q, c["pool"], bt, idx, **kw)
     torch.cuda.synchronize()

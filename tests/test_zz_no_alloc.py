@@ -41,7 +41,7 @@ def call(lib, c, noalloc):
     args = [q.data_ptr(), b, sq, h, pool.data_ptr(), pool.shape[0], bt.data_ptr(), bt.stride(0),
             bt.shape[1], seq.data_ptr(), idx.data_ptr(), idx.shape[-1], lens.data_ptr(),
             ptr(spool), 0 if spool is None else spool.shape[0], ptr(sidx), width, None,
-            sink.data_ptr(), freqs.data_ptr(), freqs.numel() // 32, 1 / np.sqrt(512)]
+            sink.data_ptr(), freqs.data_ptr(), freqs.numel() // 32, None, 1 / np.sqrt(512)]
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream().cuda_stream
     if noalloc:
@@ -94,7 +94,7 @@ def test_noalloc_decode_refuses_split_plans_beyond_its_array():
     st = lib.rm_remnant_sparse_decode_swa_noalloc_fwd(
         q.data_ptr(), tokens, 1, heads, pool.data_ptr(), 1, bt.data_ptr(), 1, 1, None,
         idx.data_ptr(), topk, None, swa_pool.data_ptr(), 1, widx.data_ptr(), wtop, None, None,
-        None, 0, 0.1, out.data_ptr(), lse.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        None, 0, None, 0.1, out.data_ptr(), lse.data_ptr(), torch.cuda.current_stream().cuda_stream)
     assert st == -5
     torch.cuda.synchronize()
     assert torch.all(out.float() == 3.0)  # nothing was launched
