@@ -12,11 +12,16 @@ Also reported on the same JSON line:
                 rocprofv3 counter runs when available);
   kernels       per-kernel timings (pack from BF16 and from FP32 input,
                 reconstruct, reconstruct + RoPE);
-  decode        Direct packed vs Native sparse decode: batch 1 (16 heads, top-k
-                2048, 8192-record context), batch 64 (log-uniform 4k-128k token
-                contexts), batch 128 x next-n 2 at 128k-token contexts on a
-                pool sized to most of HBM (capacity case), and the reference's
-                own decode shapes (H64/H128 x B8/B16, top-k 512, window rows);
+  decode        Direct packed (RoPE from the table rows, and from positions)
+                vs Native sparse decode: batch 1 (16 heads, top-k 2048,
+                8192-record context), batch 64 (log-uniform 4k-128k token
+                contexts), batch 128 x next-n 2 at 128k-token contexts (records
+                resident in a pool filling HBM), and the reference's own decode
+                shapes (H64/H128 x B8/B16, top-k 512, window rows), timed by the
+                reference's paired protocol (10 warmups, 30 interleaved rounds,
+                samples, mean/median/stdev/p5/p95 and per-round ratios);
+  store         the reference's 25 store cases, fused Packed store vs Native
+                store on the same FP32 rows, by the same protocol;
   cpu_baseline  the CPU oracle's pack + reconstruct on a bounded sample of the
                 same workload, and its decode at batch 1 and 64, each on one
                 thread and on all of this host's cores.
@@ -76,6 +81,8 @@ def parse():
                    help="survivor profile of the bulk leg (64..448, step 64)")
     p.add_argument("--decode-only", action="store_true",
                    help="only the decode cases (for kernel profiling)")
+    p.add_argument("--store-only", action="store_true",
+                   help="only the reference's store cases")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 512 MiB device copy (counter calibration)")
     return p.parse_args()
@@ -209,53 +216,105 @@ def build_decode(torch, remnant, contexts, q_len, topk, packed, seed, pool_pages
     return c
 
 
-def time_decode(torch, remnant, c, reps=10, warm=5, samples=20, rope="positions"):
-    """Median µs per decode call, from HIP-graph replays of `reps` calls.
-    Packed tails rotate by angles computed from the positions (rope
-    "positions") or by the table's rows ("table")."""
+def stats(xs):
+    """Summary of timing samples (µs): the samples in round order, mean, median,
+    stdev, p5 and p95 (the reference's per-path record, timing.json paths.*)."""
+    import numpy as np
+    a = np.asarray(xs, dtype=np.float64)
+    return {"samples": [round(float(v), 4) for v in a], "mean": float(a.mean()),
+            "median": float(np.median(a)), "stdev": float(a.std(ddof=1)) if a.size > 1 else 0.0,
+            "p5": float(np.percentile(a, 5)), "p95": float(np.percentile(a, 95))}
+
+
+def paired_timing(torch, paths, calls, graph=True, warmup=10, rounds=30):
+    """The reference's protocol (decode-store README.md:11-12): `warmup` untimed
+    rounds, then `rounds` rounds in which every path takes one sample, the
+    paths interleaved (their order reversed every other round). A sample is
+    `calls` calls of the path -- one HIP-graph replay of them (graph=True) or
+    eager launches -- timed with HIP events on the current stream, in µs per
+    call. Returns {path: [samples]}."""
+    runners = {}
+    for name, fn in paths.items():
+        if graph:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    fn()
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(calls):
+                    fn()
+            runners[name] = g.replay
+            runners[name + "@graph"] = g  # keep the graph alive
+        else:
+            runners[name] = (lambda f: lambda: [f() for _ in range(calls)])(fn)
+    names = list(paths)
+    for _ in range(warmup):
+        for n in names:
+            runners[n]()
+    torch.cuda.synchronize()
+    samples = {n: [] for n in names}
+    for r in range(rounds):
+        for n in (names if r % 2 == 0 else names[::-1]):
+            e = events(torch, 2)
+            e[0].record()
+            runners[n]()
+            e[1].record()
+            e[1].synchronize()
+            samples[n].append(e[0].elapsed_time(e[1]) * 1e3 / calls)
+    return samples
+
+
+def paired_report(samples, ratios):
+    """Per-path stats and, for each (a, b) in `ratios`, the per-round ratio a / b."""
+    out = {"paths": {n: stats(v) for n, v in samples.items()}, "paired_ratios": {}}
+    for a, b in ratios:
+        r = [x / y for x, y in zip(samples[a], samples[b])]
+        out["paired_ratios"][f"{a}_over_{b}"] = stats(r)
+    return out
+
+
+def decode_calls(torch, remnant, c):
+    """One decode call per path on case c (its own outputs and workspace):
+    Packed cases give 'direct_packed' (tails rotated from the RoPE table rows)
+    and 'direct_packed_rope_positions' (from positions and inverse
+    frequencies), Native cases 'native'."""
     tokens, heads = c["q"].shape[0] * c["q"].shape[1], c["q"].shape[2]
     _, need = remnant.get_decode_metadata(tokens, heads, c["idx"].shape[-1], c["swa"])
-    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
-    out = torch.empty_like(c["q"])
-    lse = torch.empty(c["q"].shape[:3], dtype=torch.float32, device="cuda")
-    kw = dict(seqlens=c["seqlens"], topk_length=c["lens"], sink=c["sink"], out=out, lse=lse,
-              workspace=ws)
-    if c["swa"]:
-        kw.update(swa_pool=c["swa_pool"], swa_indices=c["swa_idx"])
-
-    if c["packed"]:
-        kw.update({"rope_inv_freq": c["inv_freq"]} if rope == "positions"
-                  else {"freqs_cis": c["freqs"]})
-
-    def call():
+    calls = {}
+    variants = ((("direct_packed", {"freqs_cis": c["freqs"]}),
+                 ("direct_packed_rope_positions", {"rope_inv_freq": c["inv_freq"]}))
+                if c["packed"] else (("native", {}),))
+    for name, rope in variants:
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+        out = torch.empty_like(c["q"])
+        lse = torch.empty(c["q"].shape[:3], dtype=torch.float32, device="cuda")
+        kw = dict(seqlens=c["seqlens"], topk_length=c["lens"], sink=c["sink"], out=out, lse=lse,
+                  workspace=ws, **rope)
+        if c["swa"]:
+            kw.update(swa_pool=c["swa_pool"], swa_indices=c["swa_idx"])
         if c["packed"]:
-            remnant.remnant_sparse_decode_fwd(c["q"], c["pool"], c["table"], c["idx"], **kw)
+            calls[name] = (lambda kw: lambda: remnant.remnant_sparse_decode_fwd(
+                c["q"], c["pool"], c["table"], c["idx"], **kw))(kw)
         else:
-            remnant.native_sparse_decode_fwd(c["q"], c["pool"], c["table"], c["idx"], **kw)
+            calls[name] = (lambda kw: lambda: remnant.native_sparse_decode_fwd(
+                c["q"], c["pool"], c["table"], c["idx"], **kw))(kw)
+    return calls
 
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        for _ in range(3):
-            call()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for _ in range(reps):
-            call()
-    for _ in range(warm):
-        graph.replay()
-    torch.cuda.synchronize()
-    times = []
-    for _ in range(samples):
-        e = events(torch, 2)
-        e[0].record()
-        graph.replay()
-        e[1].record()
-        e[1].synchronize()
-        times.append(e[0].elapsed_time(e[1]) * 1e3 / reps)
-    return statistics.median(times), out, lse
+
+DECODE_RATIOS = (("direct_packed", "native"), ("direct_packed_rope_positions", "native"),
+                 ("direct_packed_rope_positions", "direct_packed"))
+
+
+def time_decode_pair(torch, remnant, cp, cn, calls=100):
+    """Paired timing of the Packed (both RoPE sources) and Native decodes of the
+    same latents: 10 warmups, 30 interleaved rounds of `calls` graph-replayed
+    calls each."""
+    paths = {**decode_calls(torch, remnant, cp), **decode_calls(torch, remnant, cn)}
+    return paired_report(paired_timing(torch, paths, calls), DECODE_RATIOS)
 
 
 def decode_bytes(c, rope_table: bool):
@@ -264,6 +323,23 @@ def decode_bytes(c, rope_table: bool):
     tokens, heads = c["q"].shape[0] * c["q"].shape[1], c["q"].shape[2]
     return (c["valid"] * per + 2 * tokens * heads * 512 * 2 + c["idx"].numel() * 4
             + tokens * c["swa"] * (584 + 4))
+
+
+def decode_entry(entry, rep, cp, cn, q_len):
+    """Median µs per step and algorithmic rates from the paired samples."""
+    entry["timing"] = rep
+    batch = cp["q"].shape[0]
+    for key, c, table in (("direct_packed", cp, True), ("direct_packed_rope_positions", cp, False),
+                          ("native", cn, False)):
+        us = rep["paths"][key]["median"]
+        byt = decode_bytes(c, rope_table=table)
+        entry[key] = {"us_per_step": us, "tokens_per_s": batch * q_len / (us * 1e-6),
+                      "algorithmic_bytes": byt, "GBps": byt / (us * 1e3),
+                      "hbm_frac": byt / (us * 1e3) / HBM_PEAK_GBS}
+    for a, b in DECODE_RATIOS:
+        r = rep["paired_ratios"][f"{a}_over_{b}"]
+        entry[f"{a}_over_{b}"] = {"median": r["median"], "p5": r["p5"], "p95": r["p95"]}
+    entry["packed_over_native_time"] = entry["direct_packed_over_native"]["median"]
 
 
 def decode_leg(torch, remnant, args):
@@ -278,38 +354,40 @@ def decode_leg(torch, remnant, args):
     for name, contexts, q_len, extra in cases:
         entry = {"batch": len(contexts), "q_len": q_len, "heads": 16, "topk": 2048,
                  "context_records_mean": float(sum(contexts) / len(contexts))}
-        for packed in (True, False):
-            log(f"decode {name} packed={packed}")
-            pool_pages = None
-            if extra.get("fill_hbm"):
-                # the capacity case: a pool of this format filling the free HBM
-                # (less 8 GB for the decode's own tensors)
+        pool_pages = {True: None, False: None}
+        if extra.get("fill_hbm"):
+            # the capacity case: records resident in a pool of each format
+            # filling the free HBM (less 8 GB for the decode's own tensors),
+            # allocated one format at a time; the paired timing then runs on
+            # two pools of half that size, both resident (time does not depend
+            # on the pool size)
+            for packed in (True, False):
                 torch.cuda.empty_cache()
                 free, _ = torch.cuda.mem_get_info()
                 page = (remnant.config.PACKED_PAGE_BYTES if packed
                         else remnant.config.NATIVE_PAGE_BYTES)
-                pool_pages = (free - (8 << 30)) // page
-            c = build_decode(torch, remnant, contexts, q_len, 2048, packed, 11, pool_pages)
-            us, _, _ = time_decode(torch, remnant, c)
-            key = "direct_packed" if packed else "native"
-            byt = decode_bytes(c, rope_table=False)
-            entry[key] = {"us_per_step": us, "tokens_per_s": c["q"].shape[0] * q_len / (us * 1e-6),
-                          "algorithmic_bytes": byt, "GBps": byt / (us * 1e3),
-                          "hbm_frac": byt / (us * 1e3) / HBM_PEAK_GBS,
-                          "pool_bytes": c["pool"].nbytes(),
-                          "records_resident": c["pool"].rows}
-            if packed:
-                entry[key]["rope"] = "positions"
-                us_t, _, _ = time_decode(torch, remnant, c, rope="table")
-                entry["direct_packed_rope_table"] = {
-                    "us_per_step": us_t, "algorithmic_bytes": decode_bytes(c, True),
-                    "GBps": decode_bytes(c, True) / (us_t * 1e3)}
-            del c
-            torch.cuda.empty_cache()
-        entry["packed_over_native_time"] = entry["direct_packed"]["us_per_step"] / entry["native"]["us_per_step"]
-        if extra.get("fill_hbm"):
+                pool = remnant.LatentPool((free - (8 << 30)) // page,
+                                          fmt="remnant" if packed else "native", device="cuda")
+                key = "direct_packed" if packed else "native"
+                entry[f"{key}_pool_bytes_filling_hbm"] = pool.nbytes()
+                entry[f"{key}_records_resident"] = pool.rows
+                del pool
             entry["records_resident_packed_over_native"] = (
-                entry["direct_packed"]["records_resident"] / entry["native"]["records_resident"])
+                entry["direct_packed_records_resident"] / entry["native_records_resident"])
+            torch.cuda.empty_cache()
+            free, _ = torch.cuda.mem_get_info()
+            half = (free - (8 << 30)) // 2
+            pool_pages = {True: half // remnant.config.PACKED_PAGE_BYTES,
+                          False: half // remnant.config.NATIVE_PAGE_BYTES}
+        log(f"decode {name}")
+        cp = build_decode(torch, remnant, contexts, q_len, 2048, True, 11, pool_pages[True])
+        cn = build_decode(torch, remnant, contexts, q_len, 2048, False, 11, pool_pages[False])
+        rep = time_decode_pair(torch, remnant, cp, cn)
+        decode_entry(entry, rep, cp, cn, q_len)
+        entry["direct_packed"]["pool_bytes"] = cp["pool"].nbytes()
+        entry["native"]["pool_bytes"] = cn["pool"].nbytes()
+        del cp, cn
+        torch.cuda.empty_cache()
         res[name] = entry
     if not args.no_reference_shapes:
         res["reference_shapes"] = reference_shapes_leg(torch, remnant)
@@ -330,27 +408,141 @@ REFERENCE_DECODE_US = {  # case: (Native µs, Direct µs) on H100
 def reference_shapes_leg(torch, remnant):
     """The same eight shapes on this GPU: Direct (Packed) and Native decodes with
     64 window rows per token, 512-entry top-k lists (317 valid in the k317
-    cases) over 4096-record contexts, timed from HIP-graph replays."""
+    cases) over 4096-record contexts, timed by the paired protocol."""
     res = {}
     for name, (ref_native, ref_direct) in REFERENCE_DECODE_US.items():
         heads, batch, valid = (int(v[1:]) for v in name.split("_"))
         entry = {"heads": heads, "batch": batch, "topk": 512, "topk_length": valid,
                  "swa_rows": 64, "reference_h100_us": {"native": ref_native, "direct": ref_direct}}
+        log(f"decode reference shape {name}")
+        cs = []
         for packed in (True, False):
-            log(f"decode reference shape {name} packed={packed}")
-            c = build_decode(torch, remnant, [4096] * batch, 1, 512, packed, 17, heads=heads,
-                             swa=64)
+            c = build_decode(torch, remnant, [4096] * batch, 1, 512, packed, 17, heads=heads, swa=64)
             c["lens"].fill_(valid)
             c["valid"] = batch * valid
-            us, _, _ = time_decode(torch, remnant, c)
-            entry["direct_packed_us" if packed else "native_us"] = us
-            if packed:
-                entry["direct_packed_rope_table_us"] = time_decode(torch, remnant, c,
-                                                                   rope="table")[0]
-            del c
-            torch.cuda.empty_cache()
-        entry["packed_over_native_time"] = entry["direct_packed_us"] / entry["native_us"]
+            cs.append(c)
+        rep = time_decode_pair(torch, remnant, cs[0], cs[1])
+        entry["direct_packed_us"] = rep["paths"]["direct_packed"]["median"]
+        entry["direct_packed_rope_positions_us"] = rep["paths"]["direct_packed_rope_positions"]["median"]
+        entry["native_us"] = rep["paths"]["native"]["median"]
+        for a, b in DECODE_RATIOS:
+            r = rep["paired_ratios"][f"{a}_over_{b}"]
+            entry[f"{a}_over_{b}"] = {"median": r["median"], "p5": r["p5"], "p95": r["p95"]}
+        entry["packed_over_native_time"] = entry["direct_packed_over_native"]["median"]
+        entry["timing"] = rep
+        del cs
+        torch.cuda.empty_cache()
         res[name] = entry
+    return res
+
+
+# The reference's store cases (dsv4-flash-decode-store timing.json, suite
+# "store"; FP32 compressor rows): name -> (phase, rows, layout). Layouts: every
+# row stored; "staggered" every fourth row (rows 0, 4, ...); "no_boundary" none
+# (no C4 record completes); "shuffled" every row at shuffled slots;
+# "invalid_dest" and "padded" a quarter of the rows skipped (slot -1) at the
+# end; "all_invalid" every row skipped. The valid-row counts match the
+# reference's valid_store_rows.
+STORE_CASES = {
+    "decode-r1-all_valid": ("decode", 1, "all_valid"),
+    "decode-r8-all_valid": ("decode", 8, "all_valid"),
+    "decode-r16-all_valid": ("decode", 16, "all_valid"),
+    "decode-r24-all_valid": ("decode", 24, "all_valid"),
+    "decode-r25-all_valid": ("decode", 25, "all_valid"),
+    "decode-r32-all_valid": ("decode", 32, "all_valid"),
+    "decode-r64-all_valid": ("decode", 64, "all_valid"),
+    "decode-r128-all_valid": ("decode", 128, "all_valid"),
+    "decode-r1-staggered": ("decode", 1, "staggered"),
+    "decode-r25-staggered": ("decode", 25, "staggered"),
+    "decode-r32-staggered": ("decode", 32, "staggered"),
+    "decode-r64-staggered": ("decode", 64, "staggered"),
+    "decode-r32-no_boundary": ("decode", 32, "no_boundary"),
+    "decode-r32-shuffled": ("decode", 32, "shuffled"),
+    "decode-r32-invalid_dest": ("decode", 32, "invalid_dest"),
+    "prefill-r1-all_valid": ("prefill", 1, "all_valid"),
+    "prefill-r64-all_valid": ("prefill", 64, "all_valid"),
+    "prefill-r257-all_valid": ("prefill", 257, "all_valid"),
+    "prefill-r1024-all_valid": ("prefill", 1024, "all_valid"),
+    "prefill-r4096-all_valid": ("prefill", 4096, "all_valid"),
+    "prefill-r8192-all_valid": ("prefill", 8192, "all_valid"),
+    "prefill-r8192-shuffled": ("prefill", 8192, "shuffled"),
+    "prefill-r8192-padded": ("prefill", 8192, "padded"),
+    "prefill-r8192-invalid_dest": ("prefill", 8192, "invalid_dest"),
+    "prefill-r8192-all_invalid": ("prefill", 8192, "all_invalid"),
+}
+# the reference's H100 medians (µs): (Native store, Kernel store)
+REFERENCE_STORE_US = {
+    "decode-r1-all_valid": (3.025, 5.132), "decode-r24-all_valid": (3.010, 5.348),
+    "decode-r128-all_valid": (2.992, 5.300), "decode-r32-shuffled": (3.010, 5.267),
+    "decode-r32-invalid_dest": (3.778, 5.267), "prefill-r1024-all_valid": (7.092, 24.289),
+    "prefill-r4096-all_valid": (7.530, 49.722), "prefill-r8192-all_valid": (13.133, 92.938),
+    "prefill-r8192-padded": (10.803, 72.549),
+}
+
+
+def store_slots(rows, layout, rng):
+    """Destination slot per row (-1: skipped) in a pool of rows + 7 records."""
+    import numpy as np
+    slots = np.arange(rows, dtype=np.int32)
+    if layout == "staggered":
+        slots[np.arange(rows) % 4 != 0] = -1
+    elif layout in ("no_boundary", "all_invalid"):
+        slots[:] = -1
+    elif layout == "shuffled":
+        slots = rng.permutation(rows).astype(np.int32)
+    elif layout in ("invalid_dest", "padded"):
+        slots[rows - rows // 4:] = -1
+    return slots
+
+
+def store_leg(torch, remnant):
+    """The reference's 25 store cases: the fused Packed store (pack_rows_fused)
+    and the Native store (native_store_rows) on the same FP32 rows and slots,
+    timed by the paired protocol -- decode-phase cases as HIP-graph replays of
+    100 calls, prefill-phase cases as 20 eager calls (the reference's
+    execution) and as graph replays of 20 calls (kernel time without the host
+    launch path)."""
+    import numpy as np
+    dev = "cuda"
+    rng = np.random.default_rng(20260919)
+    g = torch.Generator(device=dev).manual_seed(20260919)
+    gc = torch.Generator().manual_seed(20260919)
+    sigma = torch.exp(torch.empty(512).uniform_(math.log(0.1), math.log(10.0), generator=gc)).to(dev)
+    w = torch.ones(512, device=dev)
+    freqs = remnant.synthetic.rope_freqs(4 * 8200).to(dev)
+    res = {}
+    for name, (phase, rows, layout) in STORE_CASES.items():
+        slots_np = store_slots(rows, layout, rng)
+        x = torch.randn(rows, 512, device=dev, generator=g) * sigma
+        slots = torch.from_numpy(slots_np).to(dev)
+        positions = torch.arange(rows, dtype=torch.int32, device=dev)
+        pages = (rows + 7 + 63) // 64
+        ppool = remnant.LatentPool(pages, device=dev)
+        npool = remnant.LatentPool(pages, fmt="native", device=dev)
+        paths = {"kernel": lambda: remnant.pack_rows_fused(x, w, 1e-6, slots, ppool),
+                 "native": lambda: remnant.native_store_rows(x, w, 1e-6, slots, positions, freqs,
+                                                             npool)}
+        entry = {"phase": phase, "rows": rows, "layout": layout, "dtype": "float32",
+                 "valid_store_rows": int((slots_np >= 0).sum()), "capacity_rows": rows + 7}
+        if phase == "decode":
+            rep = paired_report(paired_timing(torch, paths, 100), (("kernel", "native"),))
+            entry["execution"] = "graph x 100"
+        else:
+            rep = paired_report(paired_timing(torch, paths, 20, graph=False), (("kernel", "native"),))
+            entry["execution"] = "eager x 20"
+            g20 = paired_report(paired_timing(torch, paths, 20), (("kernel", "native"),))
+            entry["graph_x20"] = {"kernel_us": g20["paths"]["kernel"]["median"],
+                                  "native_us": g20["paths"]["native"]["median"],
+                                  "kernel_over_native": g20["paired_ratios"]["kernel_over_native"]["median"]}
+        entry["kernel_us"] = rep["paths"]["kernel"]["median"]
+        entry["native_us"] = rep["paths"]["native"]["median"]
+        r = rep["paired_ratios"]["kernel_over_native"]
+        entry["kernel_over_native"] = {"median": r["median"], "p5": r["p5"], "p95": r["p95"]}
+        if name in REFERENCE_STORE_US:
+            entry["reference_h100_us"] = dict(zip(("native", "kernel"), REFERENCE_STORE_US[name]))
+        entry["timing"] = rep
+        res[name] = entry
+        del ppool, npool
     return res
 
 
@@ -539,6 +731,9 @@ def main():
     if args.decode_only:
         print(json.dumps({"decode": decode_leg(torch, remnant, args)}), flush=True)
         return
+    if args.store_only:
+        print(json.dumps({"store": store_leg(torch, remnant)}), flush=True)
+        return
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_leg(torch, remnant),
                           "host_cache": host_cache_leg(torch, remnant)}), flush=True)
@@ -604,6 +799,8 @@ def main():
     }
     if not args.quick:
         line["decode"] = decode_leg(torch, remnant, args)
+        log("store cases")
+        line["store"] = store_leg(torch, remnant)
         log("prefill read + adapter")
         line["prefill"] = prefill_leg(torch, remnant)
         log("host cache transfers")
