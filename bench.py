@@ -92,15 +92,23 @@ def events(torch, n):
     return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
 
-def bulk(torch, remnant, args):
-    """Pack + reconstruct of args.records records; returns timings (ms)."""
-    dev = "cuda"
-    n = args.records
+def bulk_inputs(torch, n, dev="cuda"):
+    """The bulk workload's inputs on the GPU: n BF16 latents N(0,1) x sigma_c
+    (sigma_c log-uniform on [0.1, 10] per coordinate) and a random permutation
+    of the n pool slots, seed 20260919."""
     g = torch.Generator(device=dev).manual_seed(20260919)
     gc = torch.Generator().manual_seed(20260919)
     sigma = torch.exp(torch.empty(512).uniform_(math.log(0.1), math.log(10.0), generator=gc))
     x = (torch.randn(n, 512, device=dev, generator=g) * sigma.to(dev)).to(torch.bfloat16)
     slots = torch.randperm(n, device=dev, generator=g).to(torch.int32)
+    return x, slots
+
+
+def bulk(torch, remnant, args):
+    """Pack + reconstruct of args.records records; returns timings (ms)."""
+    dev = "cuda"
+    n = args.records
+    x, slots = bulk_inputs(torch, n, dev)
     pool = remnant.LatentPool((n + 63) // 64, device=dev, keep_count=args.keep_count)
     w = torch.ones(512, device=dev)
     out = torch.empty((n, 512), dtype=torch.bfloat16, device=dev)

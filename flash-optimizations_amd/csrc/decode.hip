@@ -1369,10 +1369,12 @@ namespace {
 // file-scope device array instead of a caller workspace. Each GPU the library
 // runs on holds its own copy until the process ends. In host code `scratch`
 // names a host-side stand-in, never the device array: its device address is
-// looked up once per device (hipGetSymbolAddress, with that device current) and
-// only that address reaches kernels. Every split writes its whole partial slot
-// before the combine reads it, so nothing needs clearing between calls; calls
-// that overlap on one GPU share the array and race.
+// looked up once per device -- the device of the call's stream -- by
+// hipGetSymbolAddress with that device current, on the first call there (so a
+// caller that captures the call in a HIP graph makes one eager call on that
+// device first), and only that address reaches kernels. Every split writes its
+// whole partial slot before the combine reads it, so nothing needs clearing
+// between calls; calls that overlap on one GPU share the array and race.
 constexpr size_t kScratchBytes = (size_t)32 << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
@@ -1380,14 +1382,21 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of `scratch` on the current device (nullptr on failure).
-void* scratch_address() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+// Device address of `scratch` on the device of `stream` (the current device
+// for the null stream); nullptr on failure.
+void* scratch_address(hipStream_t stream) {
+  int cur = -1, dev = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+  dev = cur;
+  if (stream && hipStreamGetDevice(stream, &dev) != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) return nullptr;
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    if (dev != cur && hipSetDevice(dev) != hipSuccess) return nullptr;
+    const hipError_t st = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur && hipSetDevice(cur) != hipSuccess) return nullptr;
+    if (st != hipSuccess) return nullptr;
     g_scratch_ptr[dev] = p;
   }
   return g_scratch_ptr[dev];
@@ -1411,7 +1420,7 @@ extern "C" int rm_remnant_sparse_decode_swa_noalloc_fwd(
   if (st != RM_OK) return st;
   if (need > kScratchBytes) return RM_ERR_WORKSPACE;
   void* ws = nullptr;
-  if (need > 0 && !(ws = scratch_address())) return RM_ERR_LAUNCH;
+  if (need > 0 && !(ws = scratch_address((hipStream_t)stream))) return RM_ERR_LAUNCH;
   return rm_remnant_sparse_decode_swa_fwd(q, batch, q_len, heads, pool, pool_pages, block_table,
                                           block_table_stride, max_blocks, seqlens, indices, topk,
                                           topk_length, swa_pool, swa_pool_pages, swa_indices,

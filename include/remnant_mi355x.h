@@ -269,8 +269,10 @@ int rm_remnant_sparse_decode_planes_fwd(
  * in the reference: for callers that cannot allocate (code under HIP graph
  * capture, serving loops, harnesses that forbid hipMalloc). A call whose split
  * plan needs more than 32 MiB (rm_sparse_decode_workspace_swa) returns
- * RM_ERR_WORKSPACE without launching. Calls that overlap on one GPU share the
- * array and race; calls on one stream do not. */
+ * RM_ERR_WORKSPACE without launching. The array of the stream's GPU is used;
+ * its address is looked up on the first call there, so under HIP graph
+ * capture make one eager call on that GPU first. Calls that overlap on one
+ * GPU share the array and race; calls on one stream do not. */
 int rm_remnant_sparse_decode_swa_noalloc_fwd(
     const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads, const uint8_t* pool,
     int64_t pool_pages, const int32_t* block_table, int64_t block_table_stride,

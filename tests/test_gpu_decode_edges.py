@@ -368,10 +368,11 @@ def test_decode_long_splits_refilled_table_and_second_pass(packed):
 def test_capacity_decode_b128_next_n2_pool_beyond_4gib_offsets():
     """128 requests x 2 query tokens, top-k 2048 of 32,768-record contexts, on a
     pool of 450,000 pages (9.4 GB): the requests' pages are scattered over the
-    whole pool, so most records sit past byte offset 2^32. Four requests (eight
-    tokens) are checked against the oracle from a compact copy of their pages;
-    the pack of two requests' records and a reconstruct of high slots are
-    checked byte for byte."""
+    whole pool, so most records sit past byte offset 2^32. Sixteen requests (32
+    tokens) are checked against the oracle from a compact copy of their pages,
+    for the decode rotating from the table rows and from the positions; the
+    pack of two requests' records and a reconstruct of high slots are checked
+    byte for byte."""
     banner("capacity decode B=128 x 2, 9.4 GB pool")
     batch, q_len, topk, ctx_records = 128, 2, 2048, 32768
     pool_pages = 450_000
@@ -397,13 +398,17 @@ def test_capacity_decode_b128_next_n2_pool_beyond_4gib_offsets():
     q = (torch.randn(batch, q_len, 16, 512, generator=g) * 2.0).to(torch.bfloat16)
     sink = torch.randn(16, generator=g)
     freqs = syn.rope_freqs(4 * ctx_records)
-    out, lse = remnant.remnant_sparse_decode_fwd(
-        q.to(DEV), pool, tab, torch.from_numpy(idx).to(DEV),
-        seqlens=torch.tensor(contexts, dtype=torch.int32, device=DEV),
-        topk_length=torch.from_numpy(lens).to(DEV), sink=sink.to(DEV), freqs_cis=freqs.to(DEV))
+    kw = dict(seqlens=torch.tensor(contexts, dtype=torch.int32, device=DEV),
+              topk_length=torch.from_numpy(lens).to(DEV), sink=sink.to(DEV))
+    outs = {}
+    for rope, rkw in (("table", {"freqs_cis": freqs.to(DEV)}),
+                      ("positions", {"rope_inv_freq": syn.rope_inv_freq().to(DEV)})):
+        outs[rope] = remnant.remnant_sparse_decode_fwd(q.to(DEV), pool, tab,
+                                                       torch.from_numpy(idx).to(DEV), **kw, **rkw)
     torch.cuda.synchronize()
-    assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
-    sample = [0, 41, 90, 127]
+    for out, lse in outs.values():
+        assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
+    sample = [0, 9, 17, 30, 41, 50, 63, 70, 77, 90, 99, 104, 111, 118, 122, 127]
     # compact pool of the sampled requests' pages, table remapped to it
     pages = torch.from_numpy(table[sample].ravel().astype(np.int64)).to(DEV)
     compact = pool.layer().index_select(0, pages).cpu().numpy()
@@ -413,7 +418,9 @@ def test_capacity_decode_b128_next_n2_pool_beyond_4gib_offsets():
         syn.bf16_bits(q[sample]).reshape(len(sample), q_len, 16, 512), compact, True, ctable,
         np.array([ctx_records] * len(sample), np.int32), idx[sample], sub_lens, sink.numpy(),
         torch.view_as_real(freqs).numpy(), 1 / np.sqrt(512))
-    per_row_check(out[sample].float().cpu().numpy(), ref, lse[sample].cpu().numpy(), ref_lse)
+    for rope, (out, lse) in outs.items():
+        banner(f"capacity decode rope={rope}: {2 * len(sample)} tokens against the oracle")
+        per_row_check(out[sample].float().cpu().numpy(), ref, lse[sample].cpu().numpy(), ref_lse)
     # the pack at high offsets: two requests' records against the oracle
     for b in (41, 127):
         xs = request_latents(b).float().cpu()
@@ -436,5 +443,47 @@ def test_capacity_decode_b128_next_n2_pool_beyond_4gib_offsets():
     want = oracle.unpack_gather(compact, rows.astype(np.int32).reshape(1, -1), None,
                                 np.array([rows.size], np.int32))
     assert np.array_equal(syn.bf16_bits(out_r), want)
+    del pool
+    torch.cuda.empty_cache()
+
+
+def test_native_decode_pool_beyond_4gib_offsets():
+    """The Native control decode on a pool of 300,000 pages (11.2 GB): 16
+    requests x 2 query tokens, top-k 2048 of 32,768-record contexts, the
+    requests' pages scattered over the whole pool so most records sit past byte
+    offset 2^32. Every token is checked against the oracle from a compact copy
+    of the requests' pages."""
+    banner("native decode B=16 x 2, 11.2 GB pool")
+    batch, q_len, topk, ctx_records = 16, 2, 2048, 32768
+    pool_pages = 300_000
+    contexts = [ctx_records] * batch
+    table, _ = syn.paged_requests(contexts, 480, pool_pages)
+    assert (table.astype(np.int64) * 37376 > (1 << 32)).mean() > 0.5
+    pool = remnant.LatentPool(pool_pages, fmt="native", device=DEV)
+    w = torch.ones(512, device=DEV)
+    tab = torch.from_numpy(table).to(DEV)
+    freqs = syn.rope_freqs(4 * ctx_records).to(DEV)
+    r = torch.arange(ctx_records, device=DEV, dtype=torch.int64)
+    for b in range(batch):
+        g = torch.Generator(device=DEV).manual_seed(2000 + b)
+        x = torch.randn(ctx_records, 512, device=DEV, generator=g) * 2.0
+        slot = (tab[b, r // 64].to(torch.int64) * 64 + r % 64).to(torch.int32)
+        remnant.native_store_rows(x, w, 1e-6, slot, r.to(torch.int32), freqs, pool)
+    idx, lens = syn.topk_indices(contexts, q_len, topk, seed=481)
+    g = torch.Generator().manual_seed(482)
+    q = (torch.randn(batch, q_len, 16, 512, generator=g) * 2.0).to(torch.bfloat16)
+    sink = torch.randn(16, generator=g)
+    out, lse = remnant.native_sparse_decode_fwd(
+        q.to(DEV), pool, tab, torch.from_numpy(idx).to(DEV),
+        seqlens=torch.tensor(contexts, dtype=torch.int32, device=DEV),
+        topk_length=torch.from_numpy(lens).to(DEV), sink=sink.to(DEV))
+    torch.cuda.synchronize()
+    pages = torch.from_numpy(table.ravel().astype(np.int64)).to(DEV)
+    compact = pool.layer().index_select(0, pages).cpu().numpy()
+    ctable = np.arange(table.size, dtype=np.int32).reshape(table.shape)
+    ref, ref_lse = oracle.sparse_decode(
+        syn.bf16_bits(q).reshape(batch, q_len, 16, 512), compact, False, ctable,
+        np.array(contexts, np.int32), idx, lens, sink.numpy(), None, 1 / np.sqrt(512))
+    per_row_check(out.float().cpu().numpy(), ref, lse.cpu().numpy(), ref_lse)
     del pool
     torch.cuda.empty_cache()

@@ -777,3 +777,36 @@ def test_decode_swa_large_batch_row_combine():
     assert remnant.get_decode_metadata(256, 16, 512)[0] == 1
     assert remnant.get_decode_metadata(256, 16, 512, 64)[0] == 2
     check_decode(c)
+
+
+# ---- the bench's own bulk workload ----------------------------------------------------------
+
+def test_bulk_workload_1m_records_pack_and_reconstruct_sampled():
+    """The timed bulk workload itself: 1,048,576 BF16 records packed at a random
+    permutation of all slots (each wave packing a run of 16 consecutive rows)
+    and reconstructed in full; 20,000 sampled records' bytes and rows against
+    the oracle."""
+    import bench
+    banner("bulk 1M pack + reconstruct, 20k sampled")
+    n = 1 << 20
+    x, slots = bench.bulk_inputs(torch, n, DEV)
+    pool = remnant.LatentPool(n // 64, device=DEV)
+    remnant.pack_rows_fused(x, torch.ones(512, device=DEV), 1e-6, slots, pool)
+    out = torch.empty((n, 512), dtype=torch.bfloat16, device=DEV)
+    remnant.unpack_gather_bf16(pool, slots.view(1, n), None,
+                               torch.tensor([n], dtype=torch.int32, device=DEV), None, out)
+    torch.cuda.synchronize()
+    pick = np.sort(np.random.default_rng(5).choice(n, 20000, replace=False))
+    pick_d = torch.from_numpy(pick).to(DEV)
+    xs = x.index_select(0, pick_d).cpu()
+    ss = slots.index_select(0, pick_d).cpu().numpy().astype(np.int64)
+    # the sampled records packed by the oracle into slots 0 .. 19999
+    ref = oracle_pack(xs, np.arange(pick.size, dtype=np.int32), (pick.size + 63) // 64)
+    got = pool.layer().view(-1, 328).index_select(0, torch.from_numpy(ss).to(DEV)).cpu().numpy()
+    want = ref.reshape(-1, 328)[:pick.size]
+    bad = np.nonzero((got != want).any(axis=1))[0]
+    assert bad.size == 0, f"{bad.size} records differ, first row {int(pick[bad[0]])}"
+    rows = oracle.unpack_gather(ref, np.arange(pick.size, dtype=np.int32)[None], None,
+                                np.array([pick.size], np.int32))
+    got_rows = syn.bf16_bits(out.index_select(0, pick_d))
+    assert np.array_equal(got_rows, rows)
