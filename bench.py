@@ -76,7 +76,7 @@ def parse():
                    help="only the prefill-read reconstruction and the Adapter")
     p.add_argument("--no-reference-shapes", action="store_true",
                    help="skip the reference's H64/H128 decode shapes")
-    p.add_argument("--cpu-sample", type=int, default=196608)
+    p.add_argument("--cpu-sample", type=int, default=65536)
     p.add_argument("--keep-count", type=int, default=256,
                    help="survivor profile of the bulk leg (64..448, step 64)")
     p.add_argument("--decode-only", action="store_true",
@@ -651,15 +651,30 @@ def host_cache_leg(torch, remnant):
     return res
 
 
+def cpu_time(fn, warmup, rounds):
+    """Median wall time (s) of `rounds` calls after `warmup` untimed ones."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(rounds):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), ts
+
+
 def cpu_leg(args, torch, remnant):
     """The CPU path: the oracle (plain C, a port of the reference's
     pack/reconstruct and gather-softmax-sink decode) timed on this host on
     bounded samples of the same workloads, on one thread and on every core of
-    the host's share: pack + reconstruct of ``cpu_sample`` records of the bulk
-    workload's distribution (random slots), and the decode at the batch-1 and
-    batch-64 shapes of the decode leg (16 heads, top-k 2048; the same pools,
-    built on the GPU outside the timed region; the oracle computes in double
-    precision)."""
+    the host's share (median of rounds after warmups; the reference's protocol
+    asks 10 + 30, which the all-core legs take and the one-thread legs shorten
+    to stay within tens of seconds): pack + reconstruct of ``cpu_sample``
+    records of the bulk workload's distribution (random slots), and the decode
+    at the batch-1 and batch-64 shapes of the decode leg (16 heads, top-k 2048;
+    the same pools, built on the GPU outside the timed region), in single
+    precision (the kernels' accumulation width) and in the checker's double
+    precision."""
     import numpy as np
 
     import oracle
@@ -669,17 +684,19 @@ def cpu_leg(args, torch, remnant):
     x = oracle.synthetic_latents(n)
     slots = np.random.default_rng(1).permutation(n).astype(np.int32)
     k = args.keep_count
+    reps = {threads_all: (10, 30), 1: (1, 3)}
     pr = {}
     for threads in sorted({1, threads_all}):
         oracle.set_threads(threads)
         pool = np.zeros(((n + 63) // 64, oracle.page_bytes(k)), np.uint8)
-        t0 = time.perf_counter()
-        oracle.pack_rows_paged(x, np.ones(512, np.float32), 1e-6, slots, pool, k)
-        t1 = time.perf_counter()
-        oracle.unpack_gather(pool, slots[None], None, np.array([n], np.int32), keep_count=k)
-        t2 = time.perf_counter()
-        pr[threads] = {"records_per_s": n / (t2 - t0), "pack_records_per_s": n / (t1 - t0),
-                       "reconstruct_records_per_s": n / (t2 - t1)}
+        w, r = reps[threads]
+        t_pack, _ = cpu_time(lambda: oracle.pack_rows_paged(x, np.ones(512, np.float32), 1e-6,
+                                                            slots, pool, k), w, r)
+        t_rec, _ = cpu_time(lambda: oracle.unpack_gather(pool, slots[None], None,
+                                                         np.array([n], np.int32), keep_count=k),
+                            w, r)
+        pr[threads] = {"records_per_s": n / (t_pack + t_rec), "pack_records_per_s": n / t_pack,
+                       "reconstruct_records_per_s": n / t_rec, "warmup": w, "rounds": r}
     syn = remnant.synthetic
     dec = {}
     for name, contexts in (("b1_h16_topk2048_ctx8192", [8192]),
@@ -696,22 +713,31 @@ def cpu_leg(args, torch, remnant):
         del c
         torch.cuda.empty_cache()
         entry = {"batch": len(contexts), "tokens": len(contexts)}
-        for threads in sorted({1, threads_all}):
-            oracle.set_threads(threads)
-            t0 = time.perf_counter()
-            oracle.sparse_decode(q, pool, True, table, seq, idx, lens, sink, freqs,
-                                 1 / math.sqrt(512))
-            dt = time.perf_counter() - t0
-            entry[f"threads_{threads}"] = {"us_per_step": dt * 1e6,
-                                           "tokens_per_s": len(contexts) / dt}
+        big = len(contexts) > 1
+        for prec in ("f32", "f64"):
+            oracle.set_decode_f32(prec == "f32")
+            for threads in sorted({1, threads_all}):
+                oracle.set_threads(threads)
+                w, r = (1, 1) if (threads == 1 and big) else (
+                    (2, 5) if big else reps[threads])
+                if big and threads == 1 and prec == "f64":
+                    continue  # ~4 s a round: the single-precision one-thread run stands for it
+                dt, _ = cpu_time(lambda: oracle.sparse_decode(q, pool, True, table, seq, idx,
+                                                              lens, sink, freqs,
+                                                              1 / math.sqrt(512)), w, r)
+                entry[f"{prec}_threads_{threads}"] = {"us_per_step": dt * 1e6,
+                                                      "tokens_per_s": len(contexts) / dt,
+                                                      "warmup": w, "rounds": r}
+        oracle.set_decode_f32(False)
         dec[name] = entry
     oracle.set_threads(1)
     best = pr[threads_all]
     return {"value": best["records_per_s"], "unit": "records/s", "cores": threads_all,
             "kind": "port",
             "sample": f"{n} of the 1,048,576-record pack + reconstruct workload on "
-                      f"{threads_all} threads (one thread: {pr[1]['records_per_s']:.0f} "
-                      f"records/s); decode at batch 1 and 64 in `decode`",
+                      f"{threads_all} threads, median of 30 rounds after 10 warmups (one "
+                      f"thread: {pr[1]['records_per_s']:.0f} records/s, median of 3); decode "
+                      f"at batch 1 and 64 in `decode`",
             "pack_reconstruct": {f"threads_{t}": v for t, v in pr.items()},
             "decode": dec, "host_cpus": host}
 

@@ -80,6 +80,7 @@ def lib():
                                              i64, vp, i64, i64, i64, vp, i64, vp]
         _lib.orc_normalize.argtypes = [vp, vp, vp, f32, vp]
         _lib.orc_set_threads.argtypes = [ctypes.c_int]
+        _lib.orc_set_decode_f32.argtypes = [ctypes.c_int]
         _lib.orc_get_threads.restype = ctypes.c_int
         _lib.orc_e4m3_encode_n.argtypes = [vp, i64, vp]
         _lib.orc_e4m3_dequant_n.argtypes = [vp, vp, i64, vp]
@@ -115,6 +116,12 @@ def set_threads(n: int) -> None:
 
 def get_threads() -> int:
     return int(lib().orc_get_threads())
+
+
+def set_decode_f32(on: bool) -> None:
+    """Decode arithmetic in single precision (a CPU baseline at the kernels'
+    accumulation width) instead of the checker's double precision."""
+    lib().orc_set_decode_f32(int(bool(on)))
 
 
 def _p(a: np.ndarray | None):

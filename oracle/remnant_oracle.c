@@ -65,6 +65,10 @@
 static int g_threads = 1;
 void orc_set_threads(int n) { g_threads = n > 0 ? n : 1; }
 int orc_get_threads(void) { return g_threads; }
+/* Decode arithmetic: double precision (the default, the checker's) or single
+ * precision (a CPU baseline at the GPU kernels' accumulation width). */
+static int g_decode_f32 = 0;
+void orc_set_decode_f32(int on) { g_decode_f32 = on != 0; }
 
 static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
@@ -437,10 +441,46 @@ void orc_decode_gather(const uint8_t* pool, int64_t pool_pages, int packed,
  * logits l_j = (q_h . K_j) * scale over valid rows; Z = sum exp(l_j) + exp(sink_h);
  * out_h = sum_j exp(l_j) K_j / Z; lse_h = log Z (sink == NULL: no sink term).
  * With no valid row and no sink, out = 0 and lse = -inf. V = K (same row). */
+/* The same in single precision (logits, weights, sums and output in float). */
+static void sink_attention_head_f32(const uint16_t* qh, const uint16_t* rows,
+                                    const uint8_t* valid, int64_t nk, const float* sink_h,
+                                    float scale, double* logit_scratch, double* oh,
+                                    double* lse_h) {
+    float* logit = (float*)logit_scratch;
+    float qf[HEAD_DIM], of[HEAD_DIM];
+    for (int c = 0; c < HEAD_DIM; ++c) qf[c] = orc_bf16_to_f32(qh[c]);
+    float mx = sink_h ? *sink_h : -INFINITY;
+    for (int64_t k = 0; k < nk; ++k) {
+        if (!valid[k]) continue;
+        float acc = 0.0f;
+        const uint16_t* kr = rows + k * HEAD_DIM;
+        for (int c = 0; c < HEAD_DIM; ++c) acc += qf[c] * orc_bf16_to_f32(kr[c]);
+        logit[k] = acc * scale;
+        if (logit[k] > mx) mx = logit[k];
+    }
+    for (int c = 0; c < HEAD_DIM; ++c) oh[c] = 0.0;
+    if (mx == -INFINITY) { *lse_h = -INFINITY; return; }
+    for (int c = 0; c < HEAD_DIM; ++c) of[c] = 0.0f;
+    float z = sink_h ? expf(*sink_h - mx) : 0.0f;
+    for (int64_t k = 0; k < nk; ++k) {
+        if (!valid[k]) continue;
+        const float p = expf(logit[k] - mx);
+        z += p;
+        const uint16_t* kr = rows + k * HEAD_DIM;
+        for (int c = 0; c < HEAD_DIM; ++c) of[c] += p * orc_bf16_to_f32(kr[c]);
+    }
+    for (int c = 0; c < HEAD_DIM; ++c) oh[c] = (double)(of[c] / z);
+    *lse_h = (double)(mx + logf(z));
+}
+
 /* One head of orc_sink_attention (logit: nk doubles of scratch). */
 static void sink_attention_head(const uint16_t* qh, const uint16_t* rows, const uint8_t* valid,
                                 int64_t nk, const float* sink_h, float scale, double* logit,
                                 double* oh, double* lse_h) {
+    if (g_decode_f32) {
+        sink_attention_head_f32(qh, rows, valid, nk, sink_h, scale, logit, oh, lse_h);
+        return;
+    }
     double mx = sink_h ? (double)*sink_h : -INFINITY;
     for (int64_t k = 0; k < nk; ++k) {
         if (!valid[k]) continue;

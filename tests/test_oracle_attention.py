@@ -201,3 +201,32 @@ def test_threaded_batch_loops_give_identical_results():
     for other in results[1:]:
         for a, b in zip(results[0], other):
             assert np.array_equal(a, b)
+
+
+def test_single_precision_decode_baseline_matches_double():
+    """The CPU baseline's single-precision decode (oracle.set_decode_f32) agrees
+    with the checker's double-precision decode within the decode bar, and the
+    checker's arithmetic is restored afterwards."""
+    from remnant import synthetic as syn
+    x = syn.latents(640, seed=95).float().numpy()
+    slots = np.random.default_rng(95).permutation(640).astype(np.int32)
+    pool = np.zeros((10, oracle.PAGE_BYTES), np.uint8)
+    oracle.pack_rows_paged(x, np.ones(512, np.float32), 1e-6, slots, pool)
+    q = syn.bf16_bits(syn.latents(2 * 16, seed=96) * 4).reshape(2, 1, 16, 512)
+    table = np.arange(10, dtype=np.int32).reshape(1, 10).repeat(2, 0)
+    idx = np.random.default_rng(97).integers(0, 640, (2, 1, 400)).astype(np.int32)
+    lens = np.array([400, 250], np.int32)
+    freqs = torch.view_as_real(syn.rope_freqs(4 * 640)).numpy()
+    sink = np.linspace(-1, 1, 16).astype(np.float32)
+    args = (q, pool, True, table, np.full(2, 640, np.int32), idx, lens, sink, freqs,
+            1 / np.sqrt(512))
+    ref, ref_lse = oracle.sparse_decode(*args)
+    try:
+        oracle.set_decode_f32(True)
+        out, lse = oracle.sparse_decode(*args)
+    finally:
+        oracle.set_decode_f32(False)
+    assert not np.array_equal(out, ref)  # a different evaluation
+    assert np.abs(out - ref).max() <= 1e-4 and np.abs(lse - ref_lse).max() <= 1e-4
+    again, _ = oracle.sparse_decode(*args)
+    assert np.array_equal(again, ref)
