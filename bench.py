@@ -325,6 +325,40 @@ def time_decode_pair(torch, remnant, cp, cn, calls=100):
     return paired_report(paired_timing(torch, paths, calls), DECODE_RATIOS)
 
 
+def selftest_lib():
+    """The self-test library (test and bench calibration kernels)."""
+    import ctypes
+    path = os.path.join(ROOT, "flash-optimizations_amd", "remnant", "_lib",
+                        "libremnant_selftest.so")
+    lib = ctypes.CDLL(path)
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.rmt_gather_ceiling.argtypes = [ctypes.c_int, vp, i64, vp, i64, i64, vp, vp, i64, vp, i64,
+                                       i64, vp, vp]
+    return lib
+
+
+def gather_ceiling(torch, cp, cn):
+    """The decode's gather ceiling: the same entries' record bytes read through
+    the same block tables with nothing else done (rmt_gather_ceiling), Packed
+    and Native, paired-timed like the decodes."""
+    lib = selftest_lib()
+    out = torch.empty(4096, dtype=torch.int32, device="cuda")
+
+    def call(c):
+        pool = c["pool"].layer()
+        tokens = c["q"].shape[0] * c["q"].shape[1]
+        st = lib.rmt_gather_ceiling(int(c["packed"]), pool.data_ptr(), pool.shape[0],
+                                    c["table"].data_ptr(), c["table"].stride(0),
+                                    c["table"].shape[1], c["seqlens"].data_ptr(),
+                                    c["idx"].data_ptr(), c["idx"].shape[-1], c["lens"].data_ptr(),
+                                    c["q"].shape[1], tokens, out.data_ptr(),
+                                    torch.cuda.current_stream().cuda_stream)
+        assert st == 0, st
+
+    samples = paired_timing(torch, {"packed": lambda: call(cp), "native": lambda: call(cn)}, 100)
+    return {k: stats(v)["median"] for k, v in samples.items()}
+
+
 def decode_bytes(c, rope_table: bool):
     rec = 328 if c["packed"] else 584
     per = rec + (256 if (rope_table and c["packed"]) else 0)
@@ -392,6 +426,13 @@ def decode_leg(torch, remnant, args):
         cn = build_decode(torch, remnant, contexts, q_len, 2048, False, 11, pool_pages[False])
         rep = time_decode_pair(torch, remnant, cp, cn)
         decode_entry(entry, rep, cp, cn, q_len)
+        ceil = gather_ceiling(torch, cp, cn)
+        rec_bytes = {"packed": cp["valid"] * 336, "native": cn["valid"] * 592}  # pieces read
+        entry["gather_ceiling"] = {
+            k: {"us": v, "GBps_pieces": rec_bytes[k] / (v * 1e3)} for k, v in ceil.items()}
+        for key, c in (("direct_packed", "packed"), ("direct_packed_rope_positions", "packed"),
+                       ("native", "native")):
+            entry[key]["ceiling_frac"] = ceil[c] / entry[key]["us_per_step"]
         entry["direct_packed"]["pool_bytes"] = cp["pool"].nbytes()
         entry["native"]["pool_bytes"] = cn["pool"].nbytes()
         del cp, cn

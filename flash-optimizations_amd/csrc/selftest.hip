@@ -167,6 +167,80 @@ __global__ __launch_bounds__(kThreads) void sincos_error_kernel(uint32_t first, 
   }
 }
 
+// Gather ceiling of a sparse decode's record reads (a bench calibration, not
+// part of the product library): every valid top-k entry of every token is
+// resolved through the block table like the decode resolves it (entry r of
+// token t: request t / q_len, page block_table[b, r / 64], row r % 64), then
+// the record bytes the decode copies are read with all of a wave's loads in
+// flight -- Packed: the 21 aligned 16-byte pieces covering the 328-byte record
+// (from 8 bytes before an odd row); Native: the 36 pieces of the 576-byte data
+// row and the 16-byte piece holding its scale row -- and folded by XOR into
+// one word per wave. Nothing else is done, so its time bounds what the
+// decode's memory side can reach on the same entries. Invalid entries (k >=
+// length, r < 0, r >= seqlen, no page) read nothing.
+template <bool kPacked>
+__global__ __launch_bounds__(256) void gather_ceiling_kernel(
+    const uint8_t* __restrict__ pool, int64_t pool_pages, const int32_t* __restrict__ block_table,
+    int64_t bt_stride, int64_t max_blocks, const int32_t* __restrict__ seqlens,
+    const int32_t* __restrict__ indices, int64_t topk, const int32_t* __restrict__ topk_length,
+    int64_t q_len, int64_t tokens, uint32_t* __restrict__ out) {
+  constexpr int kPieces = kPacked ? 21 : 37;
+  constexpr int kPage = kPacked ? kPageBytes : kNativePageBytes;
+  const int lane = wave_lane();
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t waves = (int64_t)gridDim.x * 4;
+  const int64_t groups_per_token = (topk + 63) / 64;
+  uint32_t acc = 0;
+  for (int64_t gi = wave; gi < tokens * groups_per_token; gi += waves) {
+    const int64_t t = gi / groups_per_token, k = (gi - t * groups_per_token) * 64 + lane;
+    const int64_t b = t / q_len;
+    int64_t len = topk_length ? topk_length[t] : topk;
+    len = len < topk ? len : topk;
+    uint64_t base = 0;  // 0: nothing to read
+    if (k < len) {
+      const int64_t r = indices[t * topk + k];
+      const int64_t seq = seqlens ? seqlens[b] : INT64_MAX;
+      if (r >= 0 && r < seq && (r >> 6) < max_blocks) {
+        const int64_t page = block_table[b * bt_stride + (r >> 6)];
+        if (page >= 0 && page < pool_pages) {
+          const int row = (int)(r & 63);
+          const uint8_t* pg = pool + page * kPage;
+          base = kPacked ? (uint64_t)(pg + row * kRecordBytes) & ~(uint64_t)15
+                         : (uint64_t)(pg + row * kNativeDataBytes);
+          if (!kPacked) base |= (uint64_t)row << 58;  // the scale row's index, top bits
+        }
+      }
+    }
+    // 64 records x kPieces pieces: load j covers pieces 64 j .. 64 j + 63 of the
+    // group, lane -> (record, piece) = divmod(64 j + lane, kPieces)
+    u32x4 v[kPieces];
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) {
+      const int c = 64 * j + lane;
+      const int rec = c / kPieces, piece = c - rec * kPieces;
+      const uint64_t rb = __shfl(base, rec, 64);
+      v[j] = u32x4{0u, 0u, 0u, 0u};
+      if (rb) {
+        const uint64_t addr = rb & (((uint64_t)1 << 58) - 1);
+        const uint8_t* src;
+        if (kPacked || piece < 36) {
+          src = (const uint8_t*)addr + 16 * piece;
+        } else {  // Native scale row: page + 64 data rows + row * 8, in its 16-byte piece
+          const int row = (int)(rb >> 58);
+          src = (const uint8_t*)(addr - (uint64_t)row * kNativeDataBytes +
+                                 kPageRecords * kNativeDataBytes + ((row * kScaleBytes) & ~15));
+        }
+        v[j] = __builtin_nontemporal_load((const u32x4*)src);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) acc ^= v[j][0] ^ v[j][1] ^ v[j][2] ^ v[j][3];
+  }
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) acc ^= __shfl_xor(acc, d, 64);
+  if (lane == 0) out[wave] = acc;
+}
+
 int status() { return hipGetLastError() == hipSuccess ? 0 : -6; }
 
 }  // namespace
@@ -236,5 +310,27 @@ extern "C" int rmt_sincos_error(uint32_t first, uint32_t end, unsigned int* err,
   if (end < first) return -2;
   hipLaunchKernelGGL(sincos_error_kernel, dim3(kBlocks), dim3(kThreads), 0, (hipStream_t)stream,
                      first, end, err);
+  return status();
+}
+
+// The gather ceiling of a decode's record reads (see gather_ceiling_kernel);
+// out: device [4 * blocks] u32, blocks = 1024 (one word per wave).
+extern "C" int rmt_gather_ceiling(int packed, const uint8_t* pool, int64_t pool_pages,
+                                  const int32_t* block_table, int64_t bt_stride,
+                                  int64_t max_blocks, const int32_t* seqlens,
+                                  const int32_t* indices, int64_t topk,
+                                  const int32_t* topk_length, int64_t q_len, int64_t tokens,
+                                  uint32_t* out, void* stream) {
+  if (pool_pages < 0 || topk < 0 || q_len < 1 || tokens < 0 || bt_stride < max_blocks) return -2;
+  if (tokens == 0 || topk == 0) return 0;
+  const dim3 grid(1024), block(256);
+  if (packed)
+    hipLaunchKernelGGL(gather_ceiling_kernel<true>, grid, block, 0, (hipStream_t)stream, pool,
+                       pool_pages, block_table, bt_stride, max_blocks, seqlens, indices, topk,
+                       topk_length, q_len, tokens, out);
+  else
+    hipLaunchKernelGGL(gather_ceiling_kernel<false>, grid, block, 0, (hipStream_t)stream, pool,
+                       pool_pages, block_table, bt_stride, max_blocks, seqlens, indices, topk,
+                       topk_length, q_len, tokens, out);
   return status();
 }
