@@ -83,6 +83,10 @@ def parse():
                    help="only the decode cases (for kernel profiling)")
     p.add_argument("--store-only", action="store_true",
                    help="only the reference's store cases")
+    p.add_argument("--rounds", type=int, default=30,
+                   help="timed rounds of the paired protocol (decode and store cases)")
+    p.add_argument("--warm-rounds", type=int, default=10,
+                   help="untimed rounds before them")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 512 MiB device copy (counter calibration)")
     return p.parse_args()
@@ -234,7 +238,10 @@ def stats(xs):
             "p5": float(np.percentile(a, 5)), "p95": float(np.percentile(a, 95))}
 
 
-def paired_timing(torch, paths, calls, graph=True, warmup=10, rounds=30):
+PROTOCOL = {"warmup": 10, "rounds": 30}  # set from --warm-rounds / --rounds
+
+
+def paired_timing(torch, paths, calls, graph=True, warmup=None, rounds=None):
     """The reference's protocol (decode-store README.md:11-12): `warmup` untimed
     rounds, then `rounds` rounds in which every path takes one sample, the
     paths interleaved (their order reversed every other round). A sample is
@@ -259,6 +266,8 @@ def paired_timing(torch, paths, calls, graph=True, warmup=10, rounds=30):
             runners[name + "@graph"] = g  # keep the graph alive
         else:
             runners[name] = (lambda f: lambda: [f() for _ in range(calls)])(fn)
+    warmup = PROTOCOL["warmup"] if warmup is None else warmup
+    rounds = PROTOCOL["rounds"] if rounds is None else rounds
     names = list(paths)
     for _ in range(warmup):
         for n in names:
@@ -794,6 +803,7 @@ def load_traffic():
 
 def main():
     args = parse()
+    PROTOCOL.update(warmup=args.warm_rounds, rounds=args.rounds)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus above 1 is not "
                                    "supported (no inter-GPU path is built)"}))
