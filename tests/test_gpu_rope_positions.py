@@ -22,7 +22,8 @@ revolutions, then v_sin_f32 / v_cos_f32). Checked here:
 
 Parity bar: the decode's, |out - ref| <= 0.02 + 0.02 |ref| and cosine >=
 0.9999 per (token, head) row where stated, else max-abs <= 0.02 and cosine >=
-0.9999 overall (BASELINE tolerance; docs/report.md:20).
+0.9999 overall (the stated decode tolerance; the reference checks attention at
+atol = rtol = 0.02, docs/report.md:20).
 """
 
 import ctypes
