@@ -8,8 +8,9 @@
 //   l_j = (q_h . K_j) * scale, Z = sum_j exp(l_j) + exp(sink_h),
 //   out = sum_j exp(l_j) K_j / Z, lse = ln Z.
 //
-// Work split. A workgroup of six waves owns (split, token, 16-head block) and
-// walks its share of the top-k list in stages of 32 records:
+// Work split. A workgroup of six waves (eight for Packed splits at 16 heads)
+// owns (split, token, 16-head block) and walks its share of the top-k list in
+// stages of 32 records:
 //   * record metadata (index -> block table -> page/row, validity) for the
 //     share is resolved once into LDS; invalid records and slots past the end
 //     point at a readable stand-in and are masked to zero;
@@ -24,6 +25,12 @@
 //     UE8M0 scale, the tail pairs are rotated (Packed: by the table row, or
 //     with inverse frequencies by the cos and sin of the angle from the
 //     record's position, computed in the lane) or copied as stored (Native);
+//   * Packed splits at 16 heads add two tail waves on the two SIMDs whose
+//     producers have no consumer beside them: each expands and rotates the
+//     64-coordinate tails of 16 records of the stage straight from the
+//     staged rows (and in table mode copies their RoPE rows), so the
+//     producers expand only the 448 other coordinates (B=64 29.8 -> 28.5 us
+//     from positions, 29.9 -> 29.5 us from the table);
 //   * two consumer waves each own 256 of the 512 output coordinates. Both
 //     compute S^T = K Q^T for every tile on v_mfma_f32_16x16x32_bf16 (Q in
 //     registers), take weights against a fixed per-head reference (the first
@@ -171,12 +178,19 @@ __device__ __forceinline__ void wait_vm_upto() {
 constexpr int kPcProducers = 4;
 constexpr int kPcMaxGroups = 2;            // 16-head groups per workgroup (1 or 2)
 // Consumer waves and threads of a workgroup serving kHG groups of 16 heads:
-// two consumer waves per group (one per half of the output coordinates).
-template <int kHG>
+// two consumer waves per group (one per half of the output coordinates), and
+// with kHelp two tail waves (the Packed tails expanded and rotated apart from
+// the expansion waves).
+template <int kHG, bool kHelp = false>
 struct PcRoles {
   static constexpr int kConsumers = 2 * kHG;
-  static constexpr int kThreads = 64 * (kConsumers + kPcProducers);
+  static constexpr int kHelpers = kHelp ? 2 : 0;
+  static constexpr int kThreads = 64 * (kConsumers + kPcProducers + kHelpers);
 };
+// Tail waves serve Packed splits at 16 heads (an eight-wave workgroup keeps
+// 256 registers per wave).
+template <bool kPacked, int kHG>
+constexpr bool kTailWaves = kPacked && kHG == 1;
 constexpr int kPcStage = 32;               // records per stage: two 16-record tiles
 constexpr int kPcRing = 4;                 // K tile slots (two stages)
 constexpr int kPcKPitch = kHeadDim + 16;   // BF16 per K row (1056 B: rows 8 banks apart)
@@ -248,18 +262,22 @@ __device__ __forceinline__ float max_over_rows(float x) {
 // One workgroup's share: split `split` of list `a` (a C4 top-k list through
 // the block table, or with a.block_table == nullptr a list of pool slots), for
 // kHG groups of 16 heads: every expanded record serves all of them.
-template <bool kPacked, int kHG, bool kPlanes = false, bool kLong = false, bool kPos = false>
+template <bool kPacked, int kHG, bool kPlanes = false, bool kLong = false, bool kPos = false,
+          bool kHelp = false>
 __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>* sm,
                                           const int split) {
+  static_assert(!kHelp || kTailWaves<kPacked, kHG>, "tail waves: Packed, 16 heads");
   static_assert(kPacked || !kPlanes, "planes hold Packed records");
   static_assert(kPacked || !kPos, "Native records store a rotated tail");
   using G = PcGeo<kPacked>;
   // global loads per stage in a producer's in-order stream: the copies, plus
   // the Native scale row or (table mode) the two Packed RoPE row loads
-  constexpr int kRopeLoads = kPacked && !kPos ? 2 : 0;
+  // (table mode: the RoPE row loads, made by the tail waves when there are some)
+  constexpr bool kRopeRows = kPacked && !kPos && !kHelp;
+  constexpr int kRopeLoads = kRopeRows ? 2 : 0;
   constexpr int kLoads = G::kCopies + (kPacked ? kRopeLoads : 1);
-  constexpr int kPcConsumers = PcRoles<kHG>::kConsumers;
-  constexpr int kPcThreads = PcRoles<kHG>::kThreads;
+  constexpr int kPcConsumers = PcRoles<kHG, kHelp>::kConsumers;
+  constexpr int kPcThreads = PcRoles<kHG, kHelp>::kThreads;
   auto& ktile = sm->ktile;
   auto& raw = sm->raw;
   auto& sel_tab = sm->sel_tab;
@@ -388,12 +406,22 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
   // frequencies), loaded with the table and retired before the stage loop (the
   // empty asm reads it once, so the compiler's own wait for it is not repeated
   // inside the loop)
-  f32x4 theta = {0.f, 0.f, 0.f, 0.f};
-  if (kPos && a.inv_freq) theta = *(const f32x4*)(a.inv_freq + 4 * (lane >> 3));
+  // (tail waves: lane q = lane % 4 rotates the pairs 8 q .. 8 q + 7 of tail
+  // chunks 2 q and 2 q + 1, theta and theta2)
+  const bool tail_wave = kHelp && wv >= kPcConsumers + kPcProducers;
+  f32x4 theta = {0.f, 0.f, 0.f, 0.f}, theta2 = theta;
+  if (kPos && a.inv_freq) {
+    if (tail_wave) {
+      theta = *(const f32x4*)(a.inv_freq + 8 * (lane & 3));
+      theta2 = *(const f32x4*)(a.inv_freq + 8 * (lane & 3) + 4);
+    } else {
+      theta = *(const f32x4*)(a.inv_freq + 4 * (lane >> 3));
+    }
+  }
   build_table();
   wait_vm();
   __syncthreads();
-  if constexpr (kPos) asm volatile("" : "+v"(theta));
+  if constexpr (kPos) asm volatile("" : "+v"(theta), "+v"(theta2));
 
   // Splits of more than kPcMaxChunk records: consumer 0 refills the table
   // ring ahead of the producers, after its MFMA work of each step s. It
@@ -444,9 +472,148 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
     return __ballot(over) != 0;
   };
 
-  // The two roles run separate loops with the same barrier sequence per pass
+  // The roles run separate loops with the same barrier sequence per pass
   // (stages + 1 ring barriers, then two around the overflow test), so consumer
   // state (O) is never live in producers.
+  if constexpr (kHelp) {
+    if (tail_wave) {
+      // ================= tail wave =================
+      // Tail wave hh expands and rotates the 64-coordinate tails (bitmap word
+      // 7) of the 16 records of expansion waves 2 hh and 2 hh + 1, straight
+      // from their staged rows: lane (record k = lane / 4, quarter q = lane %
+      // 4) does tail chunks 2 q and 2 q + 1 (RoPE pairs 8 q .. 8 q + 7). The
+      // stage's copies have landed once its ring barrier is passed (every
+      // expansion wave waits for its own before the barrier), and the
+      // expansion waves write no tail chunk, so the step needs no other
+      // synchronisation. On splits of at most 512 records the tail waves issue
+      // ahead of the expansion waves on their SIMDs (B=64 29.1 -> 28.8 us from
+      // positions; at the expansion waves' priority no change).
+      if constexpr (!kLong) __builtin_amdgcn_s_setprio(3);
+      const int hh = wv - kPcConsumers - kPcProducers;
+      const int k = lane >> 2, q = lane & 3;
+      const int pp = 2 * hh + (k >> 3), pi = k & 7;
+      // Table mode: the lane copies bytes 64 q .. 64 q + 63 of its record's
+      // RoPE row HBM -> LDS as four 16-byte pieces into a two-stage ring of its
+      // own, two stages ahead (stages past the end copy Q), so a step waits
+      // only for the four loads issued after its own.
+      auto tring = [&](int S, int u) {
+        return lds_addr(&sm->rope_ring[((hh * 2 + S) * 4 + u) * 1024]);
+      };
+      auto tissue = [&](int s, int S) {
+        const int slot = (s * kPcStage + 8 * pp + pi) & (kPcMaxChunk - 1);
+        const uint64_t row = s < stages ? aux_tab[slot] : (uint64_t)a.q;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dma16((const void*)(row + 64 * q + 16 * u), tring(S, u));
+      };
+      auto tail = [&](int s, auto bufc) {
+        constexpr int B = decltype(bufc)::value;
+        const uint8_t* st = &raw[pp][B][0] + pi * G::kPitch;
+        const int slot = (s * kPcStage + 8 * pp + pi) & (kPcMaxChunk - 1);
+        const uint64_t row = row_tab[slot];
+        const bool valid = !(row & 1u), odd = !kPlanes && (row & 8u) != 0;
+        const bool sodd = kPlanes ? (((row - (uint64_t)a.pool) >> 8) & 1u) != 0 : odd;
+        // codes and bitmap of a contiguous record from an odd pool row sit 8
+        // bytes in; planes stage the bitmap at 256 and the scale row at 320
+        const uint8_t* bm = st + kCodeBytes + (odd ? 8 : 0);
+        const uint64_t wa = *(const uint64_t*)(bm + 16 * q);
+        const uint64_t wb = *(const uint64_t*)(bm + 16 * q + 8);
+        const uint64_t w7r = *(const uint64_t*)(bm + 56);
+        const uint32_t sw = *(const uint32_t*)(st + kDataBytes + (sodd ? 8 : 0) + 4);
+        const uint64_t w7 = valid ? w7r : 0u;
+        // codes before the tail: the record's total (its four lanes' words)
+        // less word 7's
+        int cnt = valid ? __popcll(wa) + __popcll(wb) : 0;
+        cnt += __builtin_amdgcn_update_dpp(0, cnt, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+        cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+        const int before = cnt - __popcll(w7);
+        // chunk c of word 7 is byte 7 - c (coordinate i of it: bit 7 - i)
+        const uint32_t b0 = (uint32_t)(w7 >> (56 - 16 * q)) & 0xffu;
+        const uint32_t b1 = (uint32_t)(w7 >> (48 - 16 * q)) & 0xffu;
+        const int pre0 = q == 0 ? 0 : __popcll((w7 >> 1) >> (63 - 16 * q));  // bytes 7 .. 8 - 2q
+        const float scale = exp2i((int)(valid ? sw >> 24 : 0u) - 127);
+        uint16_t* const krow = &ktile[(2 * s + (pp >> 1)) % kPcRing][0] +
+                               (8 * (pp & 1) + pi) * kPcKPitch;
+        const uint32_t r0 = lds_addr(st) + (odd ? 8u : 0u) + (uint32_t)(before + pre0);
+        const uint32_t r1 = r0 + (uint32_t)__popc(b0);
+        // (cos, sin) of the eight pairs: from the position (0 for an invalid
+        // record, whose tail is zero), or from the table row (the identity
+        // without a table)
+        float cs[16];
+        if constexpr (kPos) {
+          const float pos = u2f((uint32_t)aux_tab[slot]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            rope_sincos(pos * theta[e], cs[2 * e + 1], cs[2 * e]);
+            rope_sincos(pos * theta2[e], cs[8 + 2 * e + 1], cs[8 + 2 * e]);
+          }
+        } else {
+          wait_vm_upto<4>();  // this stage's rows: the next stage's four loads remain
+          wave_lds_sync();
+          const bool rope = a.freqs != nullptr;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const f32x4 f = *(const f32x4*)(sm->rope_ring + ((hh * 2 + (B & 1)) * 4 + u) * 1024 +
+                                            16 * lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cs[4 * u + e] = rope ? f[e] : ((e & 1) ? 0.f : 1.f);
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t r = h ? r1 : r0;
+          const lds_u32* cw = (const lds_u32*)(uintptr_t)(r & ~3u);
+          const uint64_t sel = sel_tab[h ? b1 : b0];
+          const uint32_t lo4 = __builtin_amdgcn_alignbyte(cw[1], cw[0], r);
+          const uint32_t hi4 = __builtin_amdgcn_alignbyte(cw[2], cw[1], r);
+          const uint32_t lo = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)sel);
+          const uint32_t hi = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)(sel >> 32));
+          const u32x4 v = {cvt2<false>(lo, scale), cvt2<true>(lo, scale), cvt2<false>(hi, scale),
+                           cvt2<true>(hi, scale)};
+          float x8[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x8[2 * e] = u2f(v[e] << 16);
+            x8[2 * e + 1] = u2f(v[e] & 0xffff0000u);
+          }
+          rope4(x8, cs + 8 * h);
+          const bf16x8 rot = {(__bf16)x8[0], (__bf16)x8[1], (__bf16)x8[2], (__bf16)x8[3],
+                              (__bf16)x8[4], (__bf16)x8[5], (__bf16)x8[6], (__bf16)x8[7]};
+          *(bf16x8*)(krow + kchunk(kNopeDim / 8 + 2 * q + h)) = rot;
+        }
+      };
+      auto tstep = [&](int s, auto bufc) {
+        constexpr int B = decltype(bufc)::value;
+        block_sync_lds();  // the stage's copies landed, its ring slots free
+        if (s < stages) tail(s, bufc);
+        if constexpr (!kPos) tissue(s + 2, B & 1);  // into the slot just read
+      };
+      for (int pass = 0; pass < 2; ++pass) {
+        if constexpr (!kPos) {
+          tissue(0, 0);
+          tissue(1, 1);
+        }
+        for (int s0 = 0; s0 <= stages; s0 += 4) {
+          tstep(s0, std::integral_constant<int, 0>{});
+          if (s0 + 1 <= stages) tstep(s0 + 1, std::integral_constant<int, 1>{});
+          if (s0 + 2 <= stages) tstep(s0 + 2, std::integral_constant<int, 2>{});
+          if (s0 + 3 <= stages) tstep(s0 + 3, std::integral_constant<int, 3>{});
+        }
+        wait_vm();  // drain the copies past the end
+        if (stages <= 1) break;  // as the other roles
+        __syncthreads();  // consumers' maxima published
+        float mtrue;
+        const bool redo = redo_pass(mtrue);
+        __syncthreads();
+        if (!redo) break;
+        if (long_split) {
+          build_table();
+          wait_vm();
+          __syncthreads();
+        }
+      }
+      return;
+    }
+  }
   if (wv >= kPcConsumers) {
     // ================= producer =================
     constexpr int D = G::kDepth;
@@ -580,9 +747,11 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
         const uint32_t hi4 = __builtin_amdgcn_alignbyte(gt.d2[c], gt.d1[c], gt.rk[c]);
         const uint32_t lo = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)gt.sel[c]);
         const uint32_t hi = __builtin_amdgcn_perm(hi4, lo4, (uint32_t)(gt.sel[c] >> 32));
-        *(u32x4*)(krow + kchunk(8 * pw + c)) =
-            u32x4{cvt2<false>(lo, gt.scale), cvt2<true>(lo, gt.scale), cvt2<false>(hi, gt.scale),
-                  cvt2<true>(hi, gt.scale)};
+        // (with tail waves, word 7 -- the tail -- is theirs)
+        if (!kHelp || pw != 7)
+          *(u32x4*)(krow + kchunk(8 * pw + c)) =
+              u32x4{cvt2<false>(lo, gt.scale), cvt2<true>(lo, gt.scale), cvt2<false>(hi, gt.scale),
+                    cvt2<true>(hi, gt.scale)};
       }
     };
     // Table mode: lane (i, j) copies bytes 32 j .. 32 j + 31 of record i's
@@ -705,27 +874,27 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
           head(s, bufc, h);
           gather(bufc, h, gt);
           expand(s, gt);
-          rotate(s, bufc);
+          if constexpr (!kHelp) rotate(s, bufc);
         } else {
           produce_native(s, bufc);
         }
       }
-      if constexpr (kPacked && !kPos) issue_rope(s + 2, std::integral_constant<int, B & 1>{});
+      if constexpr (kRopeRows) issue_rope(s + 2, std::integral_constant<int, B & 1>{});
     };
 
     for (int pass = 0; pass < 2; ++pass) {
       // the loads of steps -3 .. -1: copies of stages 0..2, each followed by
       // two RoPE loads (stage -1: two copies of Q into the idle ring buffer 3)
       issue_stage(0, std::integral_constant<int, 0>{});
-      if constexpr (kPacked && !kPos) {
+      if constexpr (kRopeRows) {
         const uint32_t idle = lds_addr(&raw[p][D - 1][0]);
         dma16(a.q, idle);
         dma16(a.q, idle + 1024);
       }
       issue_stage(1, std::integral_constant<int, 1>{});
-      if constexpr (kPacked && !kPos) issue_rope(0, std::integral_constant<int, 0>{});
+      if constexpr (kRopeRows) issue_rope(0, std::integral_constant<int, 0>{});
       issue_stage(2, std::integral_constant<int, 2>{});
-      if constexpr (kPacked && !kPos) issue_rope(1, std::integral_constant<int, 1>{});
+      if constexpr (kRopeRows) issue_rope(1, std::integral_constant<int, 1>{});
       for (int s0 = 0; s0 <= stages; s0 += D) {
         step(s0, std::integral_constant<int, 0>{});
         if (s0 + 1 <= stages) step(s0 + 1, std::integral_constant<int, 1>{});
@@ -918,10 +1087,11 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
 // compiled apart so that shorter splits carry none of its code. kPos: the
 // RoPE rotation from positions and inverse frequencies instead of table rows.
 template <int kHG, bool kPlanes, bool kLong, bool kPos>
-__global__ __launch_bounds__(PcRoles<kHG>::kThreads) void packed_decode_pc_kernel(DecodeArgs a) {
+__global__ __launch_bounds__((PcRoles<kHG, kTailWaves<true, kHG>>::kThreads)) void
+packed_decode_pc_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[sizeof(PcShared<true>)];
-  decode_pc<true, kHG, kPlanes, kLong, kPos>(a, reinterpret_cast<PcShared<true>*>(smem),
-                                             blockIdx.x);
+  decode_pc<true, kHG, kPlanes, kLong, kPos, kTailWaves<true, kHG>>(
+      a, reinterpret_cast<PcShared<true>*>(smem), blockIdx.x);
 }
 template <int kHG, bool kLong>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_decode_pc_kernel(DecodeArgs a) {
@@ -1282,6 +1452,8 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   hipStream_t s = (hipStream_t)stream;
   const int hg = head_groups(tokens, heads);
   const dim3 block(hg == 2 ? PcRoles<2>::kThreads : PcRoles<1>::kThreads);
+  // the split kernels of Packed decodes at 16 heads add the tail waves
+  const dim3 split_block(kPacked && hg == 1 ? PcRoles<1, true>::kThreads : block.x);
   const unsigned zblocks = (unsigned)(heads / (16 * hg));
   const bool lng = plan.chunk > kPcMaxChunk;
   if (w.topk > 0) {
@@ -1311,7 +1483,7 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
     const dim3 grid((unsigned)plan.splits, (unsigned)tokens, zblocks);
     const SplitKernel kern = lng ? split_kernel<kPacked, true>(src.planes(), hg, pos)
                                  : split_kernel<kPacked, false>(src.planes(), hg, pos);
-    hipLaunchKernelGGL(kern, grid, block, 0, s, a);
+    hipLaunchKernelGGL(kern, grid, split_block, 0, s, a);
   }
   if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   if (slots > 1) {
