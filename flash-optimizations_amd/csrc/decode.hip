@@ -266,7 +266,7 @@ template <bool kPacked, int kHG, bool kPlanes = false, bool kLong = false, bool 
           bool kHelp = false>
 __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>* sm,
                                           const int split) {
-  static_assert(!kHelp || kTailWaves<kPacked, kHG>, "tail waves: Packed, 16 heads");
+  static_assert(!kHelp || kHG == 1, "tail waves: 16-head workgroups");
   static_assert(kPacked || !kPlanes, "planes hold Packed records");
   static_assert(kPacked || !kPos, "Native records store a rotated tail");
   using G = PcGeo<kPacked>;
@@ -475,7 +475,28 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
   // The roles run separate loops with the same barrier sequence per pass
   // (stages + 1 ring barriers, then two around the overflow test), so consumer
   // state (O) is never live in producers.
-  if constexpr (kHelp) {
+  if constexpr (kHelp && !kPacked) {
+    if (tail_wave) {
+      // A launch with tail waves that runs a Native split here (the window
+      // rows of a joint launch): they only keep the barrier sequence.
+      for (int pass = 0; pass < 2; ++pass) {
+        for (int s = 0; s <= stages; ++s) block_sync_lds();
+        if (stages <= 1) break;
+        __syncthreads();
+        float mtrue;
+        const bool redo = redo_pass(mtrue);
+        __syncthreads();
+        if (!redo) break;
+        if (long_split) {
+          build_table();
+          wait_vm();
+          __syncthreads();
+        }
+      }
+      return;
+    }
+  }
+  if constexpr (kHelp && kPacked) {
     if (tail_wave) {
       // ================= tail wave =================
       // Tail wave hh expands and rotates the 64-coordinate tails (bitmap word
@@ -1100,19 +1121,20 @@ __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_decode_pc_kerne
 }
 // C4 list and window rows in one launch: workgroups x < c4.splits take a C4
 // split, the last column the window rows (Native records, one short split).
-template <bool kPacked, int kHG, bool kPlanes, bool kLong, bool kPos>
+template <bool kPacked, int kHG, bool kPlanes, bool kLong, bool kPos, bool kHelp = false>
 __device__ __forceinline__ void decode_joint(const DecodeArgs& c4, const DecodeArgs& swa) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kPcSmemBytes];
   if ((int)blockIdx.x < c4.splits)
-    decode_pc<kPacked, kHG, kPlanes, kLong, kPos>(c4, reinterpret_cast<PcShared<kPacked>*>(smem),
-                                                  blockIdx.x);
+    decode_pc<kPacked, kHG, kPlanes, kLong, kPos, kHelp>(
+        c4, reinterpret_cast<PcShared<kPacked>*>(smem), blockIdx.x);
   else
-    decode_pc<false, kHG>(swa, reinterpret_cast<PcShared<false>*>(smem), 0);
+    decode_pc<false, kHG, false, false, false, kHelp>(swa, reinterpret_cast<PcShared<false>*>(smem),
+                                                      0);
 }
 template <int kHG, bool kPlanes, bool kLong, bool kPos>
-__global__ __launch_bounds__(PcRoles<kHG>::kThreads) void packed_swa_decode_pc_kernel(
-    DecodeArgs c4, DecodeArgs swa) {
-  decode_joint<true, kHG, kPlanes, kLong, kPos>(c4, swa);
+__global__ __launch_bounds__((PcRoles<kHG, kTailWaves<true, kHG>>::kThreads)) void
+packed_swa_decode_pc_kernel(DecodeArgs c4, DecodeArgs swa) {
+  decode_joint<true, kHG, kPlanes, kLong, kPos, kTailWaves<true, kHG>>(c4, swa);
 }
 template <int kHG, bool kLong>
 __global__ __launch_bounds__(PcRoles<kHG>::kThreads) void native_swa_decode_pc_kernel(
@@ -1451,9 +1473,10 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
   a.ws_lse = bytes ? (float*)workspace + (size_t)tokens * slots * heads * kHeadDim : nullptr;
   hipStream_t s = (hipStream_t)stream;
   const int hg = head_groups(tokens, heads);
-  const dim3 block(hg == 2 ? PcRoles<2>::kThreads : PcRoles<1>::kThreads);
-  // the split kernels of Packed decodes at 16 heads add the tail waves
-  const dim3 split_block(kPacked && hg == 1 ? PcRoles<1, true>::kThreads : block.x);
+  // (Packed decodes at 16 heads add the tail waves)
+  const dim3 block(hg == 2    ? PcRoles<2>::kThreads
+                   : kPacked ? PcRoles<1, true>::kThreads
+                             : PcRoles<1>::kThreads);
   const unsigned zblocks = (unsigned)(heads / (16 * hg));
   const bool lng = plan.chunk > kPcMaxChunk;
   if (w.topk > 0) {
@@ -1483,7 +1506,7 @@ int launch_decode(const uint16_t* q, int64_t batch, int64_t q_len, int64_t heads
     const dim3 grid((unsigned)plan.splits, (unsigned)tokens, zblocks);
     const SplitKernel kern = lng ? split_kernel<kPacked, true>(src.planes(), hg, pos)
                                  : split_kernel<kPacked, false>(src.planes(), hg, pos);
-    hipLaunchKernelGGL(kern, grid, split_block, 0, s, a);
+    hipLaunchKernelGGL(kern, grid, block, 0, s, a);
   }
   if (hipGetLastError() != hipSuccess) return RM_ERR_LAUNCH;
   if (slots > 1) {
