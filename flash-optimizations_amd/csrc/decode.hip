@@ -506,10 +506,11 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
       // stage's copies have landed once its ring barrier is passed (every
       // expansion wave waits for its own before the barrier), and the
       // expansion waves write no tail chunk, so the step needs no other
-      // synchronisation. On splits of at most 512 records the tail waves issue
-      // ahead of the expansion waves on their SIMDs (B=64 29.1 -> 28.8 us from
-      // positions; at the expansion waves' priority no change).
-      if constexpr (!kLong) __builtin_amdgcn_s_setprio(3);
+      // synchronisation. The tail waves issue ahead of every other wave on
+      // their SIMDs (B=64 29.1 -> 28.8 us from positions, B=128 x next-n 2
+      // 94.7 -> 92.5 us from the table; at the expansion waves' priority of
+      // short splits no change).
+      __builtin_amdgcn_s_setprio(3);
       const int hh = wv - kPcConsumers - kPcProducers;
       const int k = lane >> 2, q = lane & 3;
       const int pp = 2 * hh + (k >> 3), pi = k & 7;
