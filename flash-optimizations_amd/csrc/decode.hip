@@ -514,20 +514,19 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
       const int hh = wv - kPcConsumers - kPcProducers;
       const int k = lane >> 2, q = lane & 3;
       const int pp = 2 * hh + (k >> 3), pi = k & 7;
-      // Table mode: the lane copies bytes 64 q .. 64 q + 63 of its record's
-      // RoPE row HBM -> LDS as four 16-byte pieces into a two-stage ring of its
-      // own, two stages ahead (stages past the end copy Q), so a step waits
-      // only for the four loads issued after its own.
-      auto tring = [&](int S, int u) {
-        return lds_addr(&sm->rope_ring[((hh * 2 + S) * 4 + u) * 1024]);
-      };
-      auto tissue = [&](int s, int S) {
+      // Table mode: the lane loads bytes 64 q .. 64 q + 63 of its record's
+      // RoPE row into registers, two stages ahead (two register sets, even
+      // and odd stages; stages past the end load Q). The tail waves issue no
+      // LDS copies, so the compiler's own waits for these loads are exact.
+      using Rows = f32x4[4];
+      auto tload = [&](int s, Rows& r) {
         const int slot = (s * kPcStage + 8 * pp + pi) & (kPcMaxChunk - 1);
         const uint64_t row = s < stages ? aux_tab[slot] : (uint64_t)a.q;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) dma16((const void*)(row + 64 * q + 16 * u), tring(S, u));
+        for (int u = 0; u < 4; ++u)  // global (not flat) loads: counted by vmcnt alone
+          r[u] = *(const __attribute__((address_space(1))) f32x4*)(row + 64 * q + 16 * u);
       };
-      auto tail = [&](int s, auto bufc) {
+      auto tail = [&](int s, auto bufc, const Rows& rr) {
         constexpr int B = decltype(bufc)::value;
         const uint8_t* st = &raw[pp][B][0] + pi * G::kPitch;
         const int slot = (s * kPcStage + 8 * pp + pi) & (kPcMaxChunk - 1);
@@ -569,16 +568,11 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
             rope_sincos(pos * theta2[e], cs[8 + 2 * e + 1], cs[8 + 2 * e]);
           }
         } else {
-          wait_vm_upto<4>();  // this stage's rows: the next stage's four loads remain
-          wave_lds_sync();
           const bool rope = a.freqs != nullptr;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const f32x4 f = *(const f32x4*)(sm->rope_ring + ((hh * 2 + (B & 1)) * 4 + u) * 1024 +
-                                            16 * lane);
+          for (int u = 0; u < 4; ++u)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) cs[4 * u + e] = rope ? f[e] : ((e & 1) ? 0.f : 1.f);
-          }
+            for (int e = 0; e < 4; ++e) cs[4 * u + e] = rope ? rr[u][e] : ((e & 1) ? 0.f : 1.f);
         }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -603,24 +597,26 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
           *(bf16x8*)(krow + kchunk(kNopeDim / 8 + 2 * q + h)) = rot;
         }
       };
-      auto tstep = [&](int s, auto bufc) {
-        constexpr int B = decltype(bufc)::value;
+      // step s: the tail of stage s from its rows, then the rows of s + 2 into
+      // the same registers
+      auto tstep = [&](int s, auto bufc, Rows& rr) {
         block_sync_lds();  // the stage's copies landed, its ring slots free
-        if (s < stages) tail(s, bufc);
-        if constexpr (!kPos) tissue(s + 2, B & 1);  // into the slot just read
+        if (s < stages) tail(s, bufc, rr);
+        if constexpr (!kPos) tload(s + 2, rr);
       };
       for (int pass = 0; pass < 2; ++pass) {
+        Rows ra, rb;  // rows of the even and odd stages (table mode)
         if constexpr (!kPos) {
-          tissue(0, 0);
-          tissue(1, 1);
+          tload(0, ra);
+          tload(1, rb);
         }
         for (int s0 = 0; s0 <= stages; s0 += 4) {
-          tstep(s0, std::integral_constant<int, 0>{});
-          if (s0 + 1 <= stages) tstep(s0 + 1, std::integral_constant<int, 1>{});
-          if (s0 + 2 <= stages) tstep(s0 + 2, std::integral_constant<int, 2>{});
-          if (s0 + 3 <= stages) tstep(s0 + 3, std::integral_constant<int, 3>{});
+          tstep(s0, std::integral_constant<int, 0>{}, ra);
+          if (s0 + 1 <= stages) tstep(s0 + 1, std::integral_constant<int, 1>{}, rb);
+          if (s0 + 2 <= stages) tstep(s0 + 2, std::integral_constant<int, 2>{}, ra);
+          if (s0 + 3 <= stages) tstep(s0 + 3, std::integral_constant<int, 3>{}, rb);
         }
-        wait_vm();  // drain the copies past the end
+        wait_vm();  // the loads past the end
         if (stages <= 1) break;  // as the other roles
         __syncthreads();  // consumers' maxima published
         float mtrue;
