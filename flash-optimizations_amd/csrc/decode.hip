@@ -287,19 +287,31 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  // Role index of this wave. A workgroup's six waves fill SIMDs 0..3 and then
-  // SIMDs 0 and 1 again, so two SIMDs hold two waves. By default the
-  // consumers are waves 0 and 1 and share those SIMDs with producers 2 and 3.
-  // Native workgroups of more than one stage put the consumers on waves 2 and
-  // 3 (a SIMD each) and the producers two per SIMD: the Native expansion is
-  // light enough to share a SIMD with another one (B=64 33.6 -> 31.4 us,
-  // B=128 x next-n 2 119.9 -> 109.1 us), the Packed one is not (35.5 -> 36.4),
-  // and single-stage splits gain nothing from it. Decided from the launch
+  // Role index of this wave. A workgroup's waves fill SIMDs 0..3 in order
+  // (hardware wave w on SIMD w % 4). By default the consumers are waves 0 and
+  // 1, producers 0..3 waves 2..5 (2 and 3 beside the consumers) and tail
+  // waves 6 and 7 (beside producers 0 and 1). Native workgroups of more than
+  // one stage put the consumers on waves 2 and 3 (a SIMD each) and the
+  // producers two per SIMD: the Native expansion is light enough to share a
+  // SIMD with another one (B=64 33.6 -> 31.4 us, B=128 x next-n 2 119.9 ->
+  // 109.1 us), the Packed one with its tail was not (35.5 -> 36.4), and
+  // single-stage splits gain nothing from it. Decided from the launch
   // arguments alone, so the consumers' Q loads start at once.
+  //
+  // Packed workgroups with tail waves (eight waves) on splits of several
+  // stages of at most 512 records: the tail waves take hardware waves 4 and 5
+  // (beside the consumers on SIMDs 0 and 1) and producers 2 and 3 waves 6 and
+  // 7 (two producers on each of SIMDs 2 and 3). A consumer slows less beside
+  // a tail wave than beside a producer: B=64 29.7 -> 28.8 us (table) and 28.4
+  // -> 28.0 us (positions). Long splits (B=128 x next-n 2 94 -> 98-102 us)
+  // and single-stage splits (B=1) keep the default placement.
   const int wv_hw = uniform(tid >> 6);
-  const bool remap =
-      !kPacked && kHG == 1 && (a.topk + kPcStage - 1) / kPcStage > (int64_t)a.splits;
-  const int wv = !remap ? wv_hw : wv_hw == 2 ? 0 : wv_hw == 3 ? 1 : wv_hw < 2 ? wv_hw + 2 : wv_hw;
+  const bool several = (a.topk + kPcStage - 1) / kPcStage > (int64_t)a.splits;
+  const bool remap = !kPacked && kHG == 1 && several;
+  const bool tail_remap = kHelp && kPacked && !kLong && several;
+  const int wv = remap ? (wv_hw == 2 ? 0 : wv_hw == 3 ? 1 : wv_hw < 2 ? wv_hw + 2 : wv_hw)
+                 : tail_remap && wv_hw >= 4 ? (wv_hw ^ 2)
+                                            : wv_hw;
   const int64_t t = blockIdx.y;
   const int64_t head_wg = (int64_t)blockIdx.z * 16 * kHG;
   // a consumer's 16 heads (consumers 2 hg and 2 hg + 1 serve group hg)
@@ -506,11 +518,11 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
       // stage's copies have landed once its ring barrier is passed (every
       // expansion wave waits for its own before the barrier), and the
       // expansion waves write no tail chunk, so the step needs no other
-      // synchronisation. The tail waves issue ahead of every other wave on
-      // their SIMDs (B=64 29.1 -> 28.8 us from positions, B=128 x next-n 2
-      // 94.7 -> 92.5 us from the table; at the expansion waves' priority of
-      // short splits no change).
-      __builtin_amdgcn_s_setprio(3);
+      // synchronisation. Beside the producers (the default placement) the
+      // tail waves issue ahead of them (B=64 29.1 -> 28.8 us from positions
+      // before the placement above, B=128 x next-n 2 94.7 -> 92.5 us from the
+      // table); beside the consumers they keep the default priority.
+      if (!tail_remap) __builtin_amdgcn_s_setprio(3);
       const int hh = wv - kPcConsumers - kPcProducers;
       const int k = lane >> 2, q = lane & 3;
       const int pp = 2 * hh + (k >> 3), pi = k & 7;
