@@ -25,12 +25,15 @@
 //     UE8M0 scale, the tail pairs are rotated (Packed: by the table row, or
 //     with inverse frequencies by the cos and sin of the angle from the
 //     record's position, computed in the lane) or copied as stored (Native);
-//   * Packed splits at 16 heads add two tail waves on the two SIMDs whose
-//     producers have no consumer beside them: each expands and rotates the
-//     64-coordinate tails of 16 records of the stage straight from the
-//     staged rows (and in table mode copies their RoPE rows), so the
-//     producers expand only the 448 other coordinates (B=64 29.8 -> 28.5 us
-//     from positions, 29.9 -> 29.5 us from the table);
+//   * Packed splits at 16 heads add two tail waves: each expands and rotates
+//     the 64-coordinate tails of 16 records of the stage straight from the
+//     staged rows (in table mode with RoPE rows it loads into registers two
+//     stages ahead), so the producers expand only the 448 other coordinates
+//     and rotate nothing. By default they sit beside the two producers that
+//     have no consumer beside them; on splits of several stages of at most
+//     512 records beside the consumers, the producers paired on the other
+//     two SIMDs (B=64 29.8 -> 27.9 us from positions, 29.9 -> 28.6 us from
+//     the table);
 //   * two consumer waves each own 256 of the 512 output coordinates. Both
 //     compute S^T = K Q^T for every tile on v_mfma_f32_16x16x32_bf16 (Q in
 //     registers), take weights against a fixed per-head reference (the first
@@ -42,7 +45,8 @@
 //   * one workgroup barrier per stage hands the ring over: producers fill
 //     stage s while consumers read stage s - 1. On splits of at most 512
 //     records the producers run at a higher wave priority than the consumers
-//     (two SIMDs hold one of each, and the producers set the stage time).
+//     (with the default placement two SIMDs hold one of each, and the
+//     producers set the stage time).
 // A Packed record (328 B, 8-byte aligned) is fetched as the 21 aligned 16-byte
 // pieces covering it: an even pool row from its start (its last piece reaches 8
 // bytes into the next row of the same page, which always exists because row 63
