@@ -137,23 +137,41 @@ __device__ __forceinline__ uint32_t fp8_pair_to_bf16(uint32_t codes, float scale
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// RN(1 / RN(sqrt(x))) for x = sumsq / 512 + eps (wave-uniform). The root is
-// the compiler's correctly rounded square root (v_sqrt_f32 alone is not: for
-// x = 1e-6 it returns the lower neighbour of RN(sqrt(x))). For
-// 2^-96 <= x < 2^128 the root s lies in [2^-48, 2^64), where one Newton step
-// from v_rcp_f32, fma(fma(-s, r0, 1), r0, r0), equals the correctly rounded
-// 1 / s; other x take the correctly rounded division.
+// RN(1 / RN(sqrt(x))) for x = sumsq / 512 + eps (wave-uniform). v_sqrt_f32
+// alone is not the correctly rounded root (for x = 1e-6 it returns the lower
+// neighbour of RN(sqrt(x))) but lies within one ulp of it. For 2^-96 <= x <
+// 2^128 the root s = v_sqrt_f32(x) is corrected by the exact FMA residuals
+// x - s' s of its neighbours s' (lower neighbour if x - s_dn s <= 0, upper if
+// x - s_up s > 0): the steps the compiler's correctly rounded square root
+// takes in that range, where it needs neither its scaling of tiny inputs nor
+// its zero and infinity cases. There the root lies in [2^-48, 2^64), where one
+// Newton step from v_rcp_f32, fma(fma(-s, r0, 1), r0, r0), equals the
+// correctly rounded 1 / s. Other x take the compiler's square root and the
+// correctly rounded division.
 __device__ __forceinline__ bool inv_root_fast_range(uint32_t xb) {
   return xb - 0x0f800000u < 0x7f800000u - 0x0f800000u;
 }
 __device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+__device__ __forceinline__ float sqrt_rn_normal(float x) {
+  const float s = __builtin_amdgcn_sqrtf(x);
+  const float sdn = u2f(f2u(s) - 1u);
+  const float sup = u2f(f2u(s) + 1u);
+  const float rdn = __builtin_fmaf(-sdn, s, x);
+  const float rup = __builtin_fmaf(-sup, s, x);
+  const float t = rdn <= 0.0f ? sdn : s;
+  return rup > 0.0f ? sup : t;
+}
+// the correctly rounded root as the store computes it
+__device__ __forceinline__ float root_rn(float x) {
+  return inv_root_fast_range(__float_as_uint(x)) ? sqrt_rn_normal(x) : sqrt_rn(x);
+}
 __device__ __forceinline__ float recip_newton(float s) {
   const float r0 = __builtin_amdgcn_rcpf(s);
   return __builtin_fmaf(__builtin_fmaf(-s, r0, 1.0f), r0, r0);
 }
 __device__ __forceinline__ float inv_root(float x) {
-  const float s = sqrt_rn(x);
-  return inv_root_fast_range(__float_as_uint(x)) ? recip_newton(s) : 1.0f / s;
+  return inv_root_fast_range(__float_as_uint(x)) ? recip_newton(sqrt_rn_normal(x))
+                                                 : 1.0f / sqrt_rn(x);
 }
 __device__ __forceinline__ float inv_rms(float sumsq, float eps) {
   const float x = sumsq * (1.0f / 512.0f) + eps;

@@ -98,7 +98,7 @@ __global__ __launch_bounds__(kThreads) void inv_root_kernel(uint32_t first, uint
        i += (uint64_t)gridDim.x * kThreads) {
     const uint32_t xb = first + (uint32_t)i;
     const float x = u2f(xb);
-    const float s = sqrt_rn(x);
+    const float s = root_rn(x);
     const float r = inv_root(x);
     const double ds = s, dr = r, dx = x;
     const double slo = 0.5 * (ds + below(s)), shi = 0.5 * (ds + above(s));
