@@ -245,8 +245,9 @@ struct PcShared {
   int32_t idx_ring[3][64];
   int32_t bt_ring[3][64];
   uint64_t sel_tab[kPacked ? 256 : 1];
-  // table mode: per producer, a two-stage ring of the RoPE row bytes its
-  // lanes rotate with ([stage % 2][half][lane] 16 bytes)
+  // table mode in workgroups without tail waves (32 heads): per producer, a
+  // two-stage ring of the RoPE row bytes its lanes rotate with ([stage %
+  // 2][half][lane] 16 bytes); the tail waves hold their rows in registers
   alignas(16) uint8_t rope_ring[kPacked ? kPcProducers * 2 * 2 * 1024 : 1];
   float mrg[2 * kPcMaxGroups][2][16];  // consumers' (reference, seen) maxima per head
 };
