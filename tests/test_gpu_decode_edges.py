@@ -181,12 +181,14 @@ def test_extreme_bitmaps_pack_reconstruct_and_decode():
 # ---- graph replay with changing inputs --------------------------------------------------------
 
 @pytest.mark.parametrize("rope", ["table", "positions"])
-@pytest.mark.parametrize("batch,heads,topk", [(8, 64, 64), (1, 16, 2048)])
+@pytest.mark.parametrize("batch,heads,topk", [(8, 64, 64), (1, 16, 2048), (32, 16, 512)])
 def test_direct_decode_graph_replay_with_changed_inputs(batch, heads, topk, rope):
     """The decode (and its split combine) captured once; q, indices, lengths
     and the records change in place between replays; every replay equals an
     eager call bit for bit and the oracle within tolerance. The tail rotation
-    comes from the table rows or (positions) from the inverse frequencies."""
+    comes from the table rows or (positions) from the inverse frequencies.
+    Splits of one stage (8 x 64 heads, batch 1) and of two stages (32 tokens,
+    8 splits: the tail waves beside the MFMA waves)."""
     banner(f"decode graph replay B={batch} H={heads} topk={topk} rope={rope}")
     rng = np.random.default_rng(420 + batch)
     contexts = [int(v) for v in rng.integers(max(topk, 200), 4 * topk + 300, batch)]
