@@ -176,21 +176,21 @@ __device__ __forceinline__ void radix_bits(const uint32_t* key, uint32_t& prefix
 
 // Seven more bits of the threshold from a histogram instead of seven
 // bit-serial counts. The threshold lies in [base, base + 128 << kShift); keys
-// in that range fall into bin (key - base) >> kShift. `above` = #{key >= base
-// + (128 << kShift)} < kK <= #{key >= base}. Keys are magnitudes: BF16 keys
-// the 15-bit pattern (one level over the binade: base = E << 7, kShift = 0),
-// FP32 keys the 31-bit one (levels with kShift = 16, 9, 2 below base = E << 23,
-// then two bit-serial steps). The wave's 128 LDS bins (zero on entry, zero
-// again on return) count the range's keys; lane l reads bins 127 - 2l and
-// 126 - 2l, so an inclusive scan over the lanes gives S(m) = #{range keys in
-// bins >= m}, and the threshold's bin is the largest m with above + S(m) >=
-// kK. On return `prefix` = base + (m << kShift), `at` = #{key >= prefix}, as
-// the bit-serial search leaves them, and `tied` = the bin's count (for BF16
-// keys, the keys equal to the threshold; otherwise the next level's range).
-template <int kK, int kShift>
-__device__ __forceinline__ void bin_histogram(const uint32_t* key, uint32_t base, int above,
-                                              uint32_t* hist, uint32_t& prefix, int& at,
-                                              int& tied) {
+// in that range fall into bin (key - base) >> kShift. Keys are magnitudes:
+// BF16 keys the 15-bit pattern (one level over the binade: base = E << 7,
+// kShift = 0), FP32 keys the 31-bit one (levels with kShift = 16, 9, 2 below
+// base = E << 23, then two bit-serial steps). The wave's 128 LDS bins (zero on
+// entry, zero again on return) count the range's keys; lane l reads bins
+// 127 - 2l and 126 - 2l, so an inclusive scan over the lanes gives S(m) =
+// #{range keys in bins >= m}, and lane 63 holds S(0), the range's keys.
+struct BinScan {
+  int incl;   // S(126 - 2 lane)
+  int lo;     // bin 126 - 2 lane
+  int hi;     // bin 127 - 2 lane
+  int total;  // S(0)
+};
+template <int kShift>
+__device__ __forceinline__ BinScan bin_scan(const uint32_t* key, uint32_t base, uint32_t* hist) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t idx = key[i] - base;
@@ -202,17 +202,37 @@ __device__ __forceinline__ void bin_histogram(const uint32_t* key, uint32_t base
   const int lane = wave_lane();
   uint64_t* const pair = (uint64_t*)(hist + 126 - 2 * lane);
   const uint64_t h = *pair;
-  *pair = 0;  // in order after the read: the bins are clear for the next record
-  const int lo = (int)(uint32_t)h, hi = (int)(uint32_t)(h >> 32);
-  const int incl = wave_inclusive_sum(lo + hi);  // S(126 - 2 lane)
-  const int need = kK - above;                   // >= 1, and S(0) >= need
-  const int l = (int)__builtin_ctzll(__ballot(incl >= need));
-  const int s_lo = __builtin_amdgcn_readlane(incl, l);         // S(126 - 2l)
-  const int s_hi = s_lo - __builtin_amdgcn_readlane(lo, l);    // S(127 - 2l)
+  *pair = 0;  // in order after the read: the bins are clear for the next range
+  BinScan b;
+  b.lo = (int)(uint32_t)h;
+  b.hi = (int)(uint32_t)(h >> 32);
+  b.incl = wave_inclusive_sum(b.lo + b.hi);
+  b.total = __builtin_amdgcn_readlane(b.incl, 63);
+  return b;
+}
+// The threshold's bin from a scan whose range holds it: `above` = #{key >= base
+// + (128 << kShift)} < kK <= above + S(0). The bin is the largest m with above
+// + S(m) >= kK. On return `prefix` = base + (m << kShift), `at` = #{key >=
+// prefix}, as the bit-serial search leaves them, and `tied` = the bin's count
+// (for BF16 keys, the keys equal to the threshold; otherwise the next level's
+// range).
+template <int kK, int kShift>
+__device__ __forceinline__ void bin_pick(const BinScan& b, uint32_t base, int above,
+                                         uint32_t& prefix, int& at, int& tied) {
+  const int need = kK - above;  // >= 1, and S(0) >= need
+  const int l = (int)__builtin_ctzll(__ballot(b.incl >= need));
+  const int s_lo = __builtin_amdgcn_readlane(b.incl, l);       // S(126 - 2l)
+  const int s_hi = s_lo - __builtin_amdgcn_readlane(b.lo, l);  // S(127 - 2l)
   const bool upper = s_hi >= need;
   prefix = base + ((uint32_t)(upper ? 127 - 2 * l : 126 - 2 * l) << kShift);
   at = above + (upper ? s_hi : s_lo);
-  tied = upper ? __builtin_amdgcn_readlane(hi, l) : __builtin_amdgcn_readlane(lo, l);
+  tied = upper ? __builtin_amdgcn_readlane(b.hi, l) : __builtin_amdgcn_readlane(b.lo, l);
+}
+template <int kK, int kShift>
+__device__ __forceinline__ void bin_histogram(const uint32_t* key, uint32_t base, int above,
+                                              uint32_t* hist, uint32_t& prefix, int& at,
+                                              int& tied) {
+  bin_pick<kK, kShift>(bin_scan<kShift>(key, base, hist), base, above, prefix, at, tied);
 }
 
 // Masked values: m[i] = v[i] where bit i of `keep` is set, else 0.
@@ -266,31 +286,49 @@ __device__ __forceinline__ uint32_t keep_at_threshold(const uint32_t* key, const
 
 // Keep mask (bit i = coordinate 8*lane + i) of the kK largest magnitudes.
 // The threshold (the kK-th largest key) is found exponent first: the previous
-// record's threshold exponent `hint` and its neighbours are tried with two or
-// three counts (consecutive records of a layer have thresholds within a
-// binade or two), then mantissa bits 22..16 come from a histogram of that
-// binade (FP32 keys: up to two more histogram levels and two bit-serial
-// steps for bits 15..0, ending at the first level whose bin holds exactly the
-// keys still needed); when the exponent is not among them the search runs
-// bit-serially over all key bits. Both ways give the same keep set. `at` is the count at the last accepted step,
-// i.e. #{key >= threshold}; only when it exceeds kK is there a boundary tie to
+// record's threshold exponent `hint` and its neighbours are tried
+// (consecutive records of a layer have thresholds within a binade or two).
+// One count at the start of the hint's binade, then the histogram of that
+// binade, whose total gives the count at its end; a second count tries the
+// binade below or above. The threshold binade's histogram
+// gives the top seven mantissa bits (FP32 keys: up to two more histogram
+// levels and two bit-serial steps for the bits below, ending at the first
+// level whose bin holds exactly the keys still needed); when the exponent is
+// none of the three the search runs bit-serially over all key bits. Both ways
+// give the same keep set. `at` is the count at the last accepted step, i.e.
+// #{key >= threshold}; only when it exceeds kK is there a boundary tie to
 // admit in coordinate order.
 template <bool kBf16, int kK>
 __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float* v, float* m,
                                                uint32_t& hint, uint32_t* hist,
                                                const uint64_t* ctab) {
-  constexpr int kExp = kBf16 ? 7 : 23;  // key bit of the exponent's LSB
-  const uint32_t e = hint;              // 1 <= e <= 252
+  constexpr int kExp = kBf16 ? 7 : 23;     // key bit of the exponent's LSB
+  constexpr int kLevel = kBf16 ? 0 : 16;   // bin width (log2) of the binade's histogram
+  const uint32_t e = hint;                 // 1 <= e <= 252
   uint32_t prefix = 0, te = 0;
   int at = 512, above = 0;
   bool found = false;
+  // The binade of `hint` first: one count at its start, and its histogram,
+  // whose total gives the count at its end.
+  BinScan bs{};
   const int c_e = count_ge(key, e << kExp);
+  int c_up = -1;
   if (c_e >= kK) {
-    const int c_up = count_ge(key, (e + 1) << kExp);
+    bs = bin_scan<kLevel>(key, e << kExp, hist);
+    c_up = c_e - bs.total;
     if (c_up < kK) {
       te = e;
       above = c_up;
       found = true;
+    }
+  }
+  if (!found) {  // the binade below or above it
+    if (c_up < 0) {
+      if (count_ge(key, (e - 1) << kExp) >= kK) {
+        te = e - 1;
+        above = c_e;
+        found = true;
+      }
     } else {
       const int c_up2 = count_ge(key, (e + 2) << kExp);
       if (c_up2 < kK) {
@@ -299,18 +337,12 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
         found = true;
       }
     }
-  } else {
-    const int c_dn = count_ge(key, (e - 1) << kExp);
-    if (c_dn >= kK) {
-      te = e - 1;
-      above = c_e;
-      found = true;
-    }
+    if (found) bs = bin_scan<kLevel>(key, te << kExp, hist);
   }
   if (found) {
     int tied;
     if (kBf16) {
-      bin_histogram<kK, 0>(key, te << 7, above, hist, prefix, at, tied);
+      bin_pick<kK, 0>(bs, te << 7, above, prefix, at, tied);
       hint = te < 1 ? 1u : (te > 252 ? 252u : te);
       return keep_at_threshold<kK>(key, v, m, prefix, at, tied, ctab);
     }
@@ -318,7 +350,7 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
     // kK: the keys at or above the bin's start are the kK largest, the next
     // key lies below the bin) ends the search: the finer levels would move
     // the prefix up to the kK-th largest key and leave the same keep set.
-    bin_histogram<kK, 16>(key, te << 23, above, hist, prefix, at, tied);
+    bin_pick<kK, 16>(bs, te << 23, above, prefix, at, tied);
     if (at != kK) {
       bin_histogram<kK, 9>(key, prefix, at - tied, hist, prefix, at, tied);
       if (at != kK) {
