@@ -117,6 +117,35 @@ def test_pack_bit_exact_many_records_per_wave_mixed_scales(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_pack_streaming_and_ordinary_calls_write_the_same_bytes(dtype):
+    """Calls of more than 131,072 rows read rows and write records with
+    streaming accesses, smaller calls with ordinary ones. 131,073 records packed
+    in one call equal the same records packed as a 131,072-row call and a 1-row
+    call, byte for byte, and 2,000 sampled records equal the oracle's."""
+    banner(f"pack streaming vs ordinary calls {dtype}")
+    n = 131073
+    x = syn.latents(n, seed=48).to(dtype).to(DEV)
+    slots_np = np.random.default_rng(48).permutation(n).astype(np.int32)
+    slots = torch.from_numpy(slots_np).to(DEV)
+    pages = (n + 63) // 64
+    w = torch.ones(512, device=DEV)
+    one = remnant.LatentPool(pages, device=DEV)
+    two = remnant.LatentPool(pages, device=DEV)
+    one.buffer.fill_(0x5A)
+    two.buffer.fill_(0x5A)
+    remnant.pack_rows_fused(x, w, 1e-6, slots, one)
+    remnant.pack_rows_fused(x[:n - 1], w, 1e-6, slots[:n - 1], two)
+    remnant.pack_rows_fused(x[n - 1:], w, 1e-6, slots[n - 1:], two)
+    torch.cuda.synchronize()
+    assert torch.equal(one.buffer, two.buffer)
+    pick = np.random.default_rng(49).choice(n, 2000, replace=False)
+    ref = oracle_pack(x[torch.from_numpy(pick).to(DEV)].cpu(), slots_np[pick], pages)
+    got = one.layer().cpu().numpy().reshape(-1, 328)
+    want = ref.reshape(-1, 328)
+    assert np.array_equal(got[slots_np[pick]], want[slots_np[pick]])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
 @pytest.mark.parametrize("eps", [0.0, 1e-6], ids=["eps0", "eps1e-6"])
 def test_pack_bit_exact_rms_root_paths(dtype, eps):
     """Row scales 2^-72 .. 2^66 put x = sum(m^2)/512 + eps below 2^-96 (the
