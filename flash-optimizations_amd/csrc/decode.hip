@@ -891,6 +891,12 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
         }
     };
 
+    // Native workgroups with paired expansion waves: waves 2 and 3 (each the
+    // second of a SIMD's pair) issue their copies after their stage's work,
+    // so the pair's first LDS waits of a stage do not coincide (B=64 27.6 ->
+    // 27.3 us, B=128 x next-n 2 93.3 -> 90.9 us). The Packed pairs, beside
+    // the tail waves' copies and reads, ran 1-3 % slower with it.
+    const bool late_copies = remap && p >= 2;
     // One stage step in ring phase B (the stage loop is unrolled by D so the
     // ring buffer of each step is fixed).
     auto step = [&](int s, auto bufc) {
@@ -901,7 +907,9 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
       wait_vm_upto<(D - 2) * kLoads + kRopeLoads>();
       wave_lds_sync();
       block_sync_lds();  // ring slots of stage s free (consumers are on stage s - 1)
-      issue_stage(s + D - 1, std::integral_constant<int, (B + D - 1) % D>{});  // past the end: fillers
+      // past the end: fillers
+      if (!late_copies)
+        issue_stage(s + D - 1, std::integral_constant<int, (B + D - 1) % D>{});
       if (s < stages) {
         if constexpr (kPacked) {
           Head h;
@@ -914,6 +922,8 @@ __device__ __forceinline__ void decode_pc(const DecodeArgs& a, PcShared<kPacked>
           produce_native(s, bufc);
         }
       }
+      if (late_copies)
+        issue_stage(s + D - 1, std::integral_constant<int, (B + D - 1) % D>{});
       if constexpr (kRopeRows) issue_rope(s + 2, std::integral_constant<int, B & 1>{});
     };
 
