@@ -320,23 +320,24 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
   constexpr int kLevel = kBf16 ? 0 : 16;   // bin width (log2) of the binade's histogram
   const uint32_t e = hint;                 // 1 <= e <= 252
   uint32_t prefix = 0, te = 0;
-  int at = 512, above = 0;
+  int at = 512, tied = 0;
   bool found = false;
   // The binade of `hint` first: one count at its start, and its histogram,
-  // whose total gives the count at its end.
-  BinScan bs{};
+  // whose total gives the count at its end. (Each histogram is picked where
+  // it is scanned: its per-lane scan values then need no merging.)
   const int c_e = count_ge(key, e << kExp);
   int c_up = -1;
   if (c_e >= kK) {
-    bs = bin_scan<kLevel>(key, e << kExp, hist);
-    c_up = c_e - bs.total;
+    const BinScan b = bin_scan<kLevel>(key, e << kExp, hist);
+    c_up = c_e - b.total;
     if (c_up < kK) {
       te = e;
-      above = c_up;
       found = true;
+      bin_pick<kK, kLevel>(b, e << kExp, c_up, prefix, at, tied);
     }
   }
   if (!found) {  // the binade below or above it
+    int above = 0;
     if (c_up < 0) {
       if (count_ge(key, (e - 1) << kExp) >= kK) {
         te = e - 1;
@@ -351,12 +352,12 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
         found = true;
       }
     }
-    if (found) bs = bin_scan<kLevel>(key, te << kExp, hist);
+    if (found)
+      bin_pick<kK, kLevel>(bin_scan<kLevel>(key, te << kExp, hist), te << kExp, above, prefix, at,
+                           tied);
   }
   if (found) {
-    int tied;
     if (kBf16) {
-      bin_pick<kK, 0>(bs, te << 7, above, prefix, at, tied);
       hint = te < 1 ? 1u : (te > 252 ? 252u : te);
       return keep_at_threshold<kK>(key, v, m, prefix, at, tied, ctab);
     }
@@ -364,7 +365,6 @@ __device__ __forceinline__ uint32_t select_top(const uint32_t* key, const float*
     // kK: the keys at or above the bin's start are the kK largest, the next
     // key lies below the bin) ends the search: the finer levels would move
     // the prefix up to the kK-th largest key and leave the same keep set.
-    bin_pick<kK, 16>(bs, te << 23, above, prefix, at, tied);
     if (at != kK) {
       bin_histogram<kK, 9>(key, prefix, at - tied, hist, prefix, at, tied);
       if (at != kK) {
