@@ -116,21 +116,24 @@ def test_pack_bit_exact_many_records_per_wave_mixed_scales(dtype):
     assert np.array_equal(got[slots[pick]], want[slots[pick]])
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
-def test_pack_streaming_and_ordinary_calls_write_the_same_bytes(dtype):
+@pytest.mark.parametrize("dtype,keep_count", [(torch.bfloat16, 256), (torch.float32, 256),
+                                              (torch.bfloat16, 448), (torch.bfloat16, 64)],
+                         ids=["bf16", "fp32", "bf16-keep448", "bf16-keep64"])
+def test_pack_streaming_and_ordinary_calls_write_the_same_bytes(dtype, keep_count):
     """Calls of more than 131,072 rows read rows and write records with
     streaming accesses, smaller calls with ordinary ones. 131,073 records packed
     in one call equal the same records packed as a 131,072-row call and a 1-row
-    call, byte for byte, and 2,000 sampled records equal the oracle's."""
-    banner(f"pack streaming vs ordinary calls {dtype}")
+    call, byte for byte, and 2,000 sampled records equal the oracle's (448
+    survivors: records of 65 eight-byte pieces, the last one a second store)."""
+    banner(f"pack streaming vs ordinary calls {dtype} keep {keep_count}")
     n = 131073
     x = syn.latents(n, seed=48).to(dtype).to(DEV)
     slots_np = np.random.default_rng(48).permutation(n).astype(np.int32)
     slots = torch.from_numpy(slots_np).to(DEV)
     pages = (n + 63) // 64
     w = torch.ones(512, device=DEV)
-    one = remnant.LatentPool(pages, device=DEV)
-    two = remnant.LatentPool(pages, device=DEV)
+    one = remnant.LatentPool(pages, device=DEV, keep_count=keep_count)
+    two = remnant.LatentPool(pages, device=DEV, keep_count=keep_count)
     one.buffer.fill_(0x5A)
     two.buffer.fill_(0x5A)
     remnant.pack_rows_fused(x, w, 1e-6, slots, one)
@@ -139,9 +142,11 @@ def test_pack_streaming_and_ordinary_calls_write_the_same_bytes(dtype):
     torch.cuda.synchronize()
     assert torch.equal(one.buffer, two.buffer)
     pick = np.random.default_rng(49).choice(n, 2000, replace=False)
-    ref = oracle_pack(x[torch.from_numpy(pick).to(DEV)].cpu(), slots_np[pick], pages)
-    got = one.layer().cpu().numpy().reshape(-1, 328)
-    want = ref.reshape(-1, 328)
+    ref = oracle_pack(x[torch.from_numpy(pick).to(DEV)].cpu(), slots_np[pick], pages,
+                      keep_count=keep_count)
+    rec = keep_count + 72
+    got = one.layer().cpu().numpy().reshape(-1, rec)
+    want = ref.reshape(-1, rec)
     assert np.array_equal(got[slots_np[pick]], want[slots_np[pick]])
 
 
